@@ -1,0 +1,147 @@
+/*
+ * spx_sampler.h — the C ABI of the MI355X (gfx950) batched token sampler.
+ *
+ * One call samples many rows of logits that already live in device memory: suppress-token masking, presence /
+ * frequency / repetition penalties over each row's token history, temperature, top-k, top-p, the softmax and the
+ * categorical draw from a caller-supplied uniform, or greedy argmax. Every row carries its own parameters and its own
+ * "flavor", the sampling semantics of one speech.cpp family:
+ *
+ *   SPX_FLAVOR_TRANSFORMERS  Qwen3-TTS talker / code predictor and Qwen3-ASR greedy decoding, as
+ *                            src/families/qwen3-tts/sampler.cpp:29-116 restates transformers' logits processors.
+ *   SPX_FLAVOR_HARU          Haru's sample_token(), src/families/haru/sampler.cpp:18-61.
+ *   SPX_FLAVOR_FISH          Drama 3's fish-speech sample_top_k_top_p(), src/families/drama3/sampler.cpp:30-60.
+ *
+ * The draw itself is src/common/sampling.cpp:9-19 (pick): the first candidate whose cumulative share of the kept
+ * weights passes u, the last where none does. u comes from the caller (src/common/sampling.cpp:5-7, uniform()),
+ * one double per row, so results are deterministic and independent of the launch shape.
+ *
+ * Conventions: no exception or C++ type crosses this boundary. Pointers named d_* are device pointers; all work is
+ * queued on the given stream and is asynchronous; the sampler handle owns a preallocated workspace and must not be
+ * used from two streams at once (calls on one handle serialize on its stream). A handle is bound to the device that
+ * was current when it was created.
+ */
+#ifndef SPX_SAMPLER_H
+#define SPX_SAMPLER_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Call-level status. */
+typedef enum spx_status {
+    SPX_OK = 0,
+    SPX_ERR_INVALID_ARGUMENT = 1, /* a null pointer, a size beyond what the handle was created for, a bad dtype */
+    SPX_ERR_DEVICE = 2,           /* a HIP call failed; spx_last_error() has its message */
+    SPX_ERR_OUT_OF_MEMORY = 3,
+} spx_status;
+
+/*
+ * Row-level status, written to d_out_status[row]. Each non-OK code stands for the exception the reference throws for
+ * that row (the C++ host layer rethrows it as the same Error kind naming the same input):
+ */
+typedef enum spx_row_status {
+    SPX_ROW_OK = 0,
+    /* Error(Fault::OutOfRange, ..., "repetition_penalty"): src/families/qwen3-tts/sampler.cpp:44-48 */
+    SPX_ROW_REP_PENALTY_OVERFLOW = 1,
+    /* temperature_overflow(): src/common/sampling.cpp:21-25, raised at qwen3-tts/sampler.cpp:83,
+       haru/sampler.cpp:34, drama3/sampler.cpp:47 */
+    SPX_ROW_TEMPERATURE_OVERFLOW = 2,
+    /* std::runtime_error("no token has a finite logit to pick from"): qwen3-tts/sampler.cpp:49 */
+    SPX_ROW_NO_FINITE_LOGIT = 3,
+    /* Error(Fault::Device, ...): haru/sampler.cpp:21-23 (NaN or +inf), drama3/sampler.cpp:35-37 (any non-finite);
+       also a NaN logit drawn under SPX_FLAVOR_TRANSFORMERS, whose reference order is undefined there */
+    SPX_ROW_NONFINITE_INPUT = 4,
+    /* parameters the reference's engines refuse before sampling (a temperature <= 0 or NaN where a draw needs one,
+       a ban list under SPX_FLAVOR_FISH, an unknown flavor) */
+    SPX_ROW_INVALID_PARAMS = 5,
+} spx_row_status;
+
+typedef enum spx_dtype { SPX_F32 = 0, SPX_BF16 = 1 } spx_dtype;
+
+typedef enum spx_flavor { SPX_FLAVOR_TRANSFORMERS = 0, SPX_FLAVOR_HARU = 1, SPX_FLAVOR_FISH = 2 } spx_flavor;
+
+/*
+ * Per-row parameters, 32 bytes. The first five fields are SamplingParams (src/families/qwen3-tts/sampler.h:12-24),
+ * haru::Sampling (src/families/haru/sampler.h:13-19) and drama3::Sampling (src/families/drama3/sampler.h:12-17).
+ * top_k <= 0 keeps every token (TRANSFORMERS, HARU); FISH clamps it to [1, vocab] as drama3/sampler.cpp:44 does.
+ * presence_penalty and frequency_penalty have no counterpart in the reference: where non-zero they are applied to the
+ * raw logit of every token that occurs c > 0 times in the history, as l = (l - frequency*c) - presence in float, before
+ * the repetition penalty. Neutral values (rep 1, presence 0, frequency 0) leave the history unread.
+ */
+typedef struct spx_row_params {
+    int32_t flavor;           /* spx_flavor */
+    int32_t greedy;           /* nonzero: argmax of the penalized, suppressed logits; u unused */
+    float temperature;
+    int32_t top_k;
+    float top_p;
+    float repetition_penalty; /* 1 = off */
+    float presence_penalty;   /* 0 = off */
+    float frequency_penalty;  /* 0 = off */
+} spx_row_params;
+
+typedef struct spx_sampler spx_sampler;
+
+/*
+ * Creates a handle on the current HIP device with a workspace for calls of at most max_rows rows of at most
+ * max_vocab logits and at most max_hist history ids per row, and room for max_out kept candidates per row in the
+ * optional candidate outputs of spx_sample_rows.
+ */
+spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, int max_hist, int max_out);
+void spx_sampler_destroy(spx_sampler * s);
+
+/*
+ * Samples `rows` rows. Replaces, batched and on the device, the per-row host calls
+ *   sample(logits, p, history, banned, u)         src/families/qwen3-tts/sampler.cpp:103-111 (and :113-116)
+ *   tokens[pick(candidates(logits, s).weights, u)] src/families/haru/sampler.h:32, drama3/sampler.h:32, :49-52
+ *   max_element(logits)                            src/families/qwen3-asr/decoder.cpp:112, greedy
+ *
+ *   d_logits       rows x vocab logits, row r at d_logits + r*ld elements of `dtype`
+ *   d_hist         the history ids of all rows, concatenated; row r's are d_hist[d_hist_off[r] .. d_hist_off[r+1]);
+ *                  ids outside [0, vocab) are skipped as restricted() skips them. May be null when every row has
+ *                  neutral penalties.
+ *   d_hist_off     rows+1 offsets into d_hist (null with d_hist)
+ *   d_banned       suppress mask, bit i%32 of word i/32 set = token i removed (-inf); row r's mask starts at
+ *                  d_banned + r*banned_stride words, so a stride of 0 shares one mask by every row. May be null.
+ *   d_params       rows spx_row_params
+ *   d_u            rows doubles in [0, 1], the uniform() of each drawing row (unread for greedy rows)
+ *   d_out_ids      rows int32: the token picked (-1 where the row status is not OK)
+ *   d_out_status   rows int32: spx_row_status
+ *   d_out_kept     optional (may be null): rows int32, the number of candidates the draw picked from
+ *   d_out_cand_ids, d_out_cand_probs   optional (both null or both set): rows x max_out, the first
+ *                  min(kept, max_out) candidates by falling logit and their weights normalized to sum 1 over the
+ *                  kept candidates (the reference's Candidates, normalized as pick() normalizes them)
+ */
+spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
+                           int64_t banned_stride, const spx_row_params * d_params, const double * d_u,
+                           int32_t * d_out_ids, int32_t * d_out_status, int32_t * d_out_kept,
+                           int32_t * d_out_cand_ids, float * d_out_cand_probs, void * stream);
+
+/*
+ * Greedy argmax of `rows` rows with a shared or per-row suppress mask: the first largest logit, NaN ignored except in
+ * the first position, as std::max_element does (src/families/qwen3-asr/decoder.cpp:112,
+ * src/common/qwen3-decoder.cpp:427-429 with the fork's first-of-equals argmax). Same layout rules as spx_sample_rows.
+ */
+spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const uint32_t * d_banned, int64_t banned_stride, int32_t * d_out_ids, void * stream);
+
+/* Message of the last failed call on this thread ("" when none). */
+const char * spx_last_error(void);
+
+/* Diagnostics of the last call on a handle (host-side copy, valid after the stream has synchronized). */
+typedef struct spx_stats {
+    int32_t rows_fallback; /* rows whose candidate set needed the multi-pass path */
+    int32_t splits;        /* work-groups per row of the streaming pass */
+    int32_t block;         /* threads per work-group */
+    int32_t reserved;
+} spx_stats;
+spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SPX_SAMPLER_H */

@@ -1,0 +1,85 @@
+/*
+ * spx_oracle.h — TEST INFRASTRUCTURE ONLY. A CPU restatement of speech.cpp's token samplers, used as the checker of
+ * the HIP sampler (tests/, __graft_entry__.smoke()) and as the timed CPU baseline of bench.py. No product code links,
+ * loads or calls it.
+ *
+ * Each function follows one reference function step by step (same copies, same float/double arithmetic, the same
+ * std::partial_sort with the same comparator, the same top-p rule) and cites it. Paths are relative to the reference
+ * checkout (nyosegawa/speech.cpp 0.11.1).
+ *
+ * Parity pins (see tests/test_oracle_*.py):
+ *   orc_uniform_fill, orc_pick        bit-exact against the reference's own src/common/sampling.cpp, compiled
+ *                                     unchanged into oracle/_ref, and the known answers of
+ *                                     checks/qwen3-tts/qwen3-tts-sampler-check.cpp:98-115
+ *   orc_tf_candidates / orc_tf_sample transformers' logits processors (installed transformers, the library the
+ *                                     reference restates) on golden fixtures; the refusals of
+ *                                     qwen3-tts-sampler-check.cpp:70-91 and qwen3-tts-graph-sampler-check.cpp:162-186;
+ *                                     closed forms (greedy = first max, top-k 1 = argmax, top-p 1 and top-k 0 = full
+ *                                     softmax) and brute force on tiny vocabularies
+ *   orc_haru_candidates               a torch restatement of sample_token() on golden fixtures within the tolerance of
+ *                                     checks/haru/haru-sampling-check.cpp:36; ties to the lower id; closed forms
+ *   orc_fish_candidates               a torch restatement of sample_top_k_top_p() on golden fixtures within the
+ *                                     tolerances of checks/drama3/drama3-sampler-check.cpp:36-41; closed forms
+ *   presence / frequency penalty      parity unpinned against any reference (the reference has none); pinned by its
+ *                                     closed form l - frequency*count - presence
+ */
+#ifndef SPX_ORACLE_H
+#define SPX_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/spx_sampler.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* n numbers of uniform() (src/common/sampling.cpp:5-7) from std::mt19937_64(seed). */
+void orc_uniform_fill(uint64_t seed, int n, double * out);
+
+/* pick() (src/common/sampling.cpp:9-19). */
+int orc_pick(const double * weights, int n, double u);
+
+/*
+ * candidates() of one flavor on one row, after the row has been through the penalty and suppression stages.
+ * Returns a spx_row_status; fills up to `cap` tokens and their unnormalized weights, and *n_out with the full count.
+ */
+int orc_tf_candidates(const float * logits, int vocab, const spx_row_params * p, const int32_t * hist, int n_hist,
+                      const uint8_t * banned, int32_t * tokens, double * weights, int cap, int * n_out);
+int orc_haru_candidates(const float * logits, int vocab, float temperature, int top_k, float top_p, int32_t * tokens,
+                        double * weights, int cap, int * n_out);
+int orc_fish_candidates(const float * logits, int vocab, float temperature, int top_k, float top_p, int32_t * tokens,
+                        double * weights, int cap, int * n_out);
+
+/* What the oracle reports about one row beyond its pick, to classify a differing pick of the device. */
+typedef struct orc_row_report {
+    int32_t id;
+    int32_t status;
+    int32_t kept;          /* candidates the draw picked from */
+    int32_t pad;
+    double boundary;       /* distance of u from the nearest boundary between two kept candidates' cumulative shares */
+    double cut;            /* distance of the top-p rule's nearest decision from its threshold (inf without one) */
+} orc_row_report;
+
+/*
+ * The batched semantics of spx_sample_rows on host memory, row by row as the reference's callers do. `threads` > 1
+ * splits the rows over that many std::threads. cand_ids/cand_probs (rows x cap) may be null.
+ */
+void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_t ld, const int32_t * hist,
+                     const int32_t * hist_off, const uint32_t * banned, int64_t banned_stride,
+                     const spx_row_params * params, const double * u, orc_row_report * reports, int32_t * cand_ids,
+                     double * cand_probs, int cap, int threads);
+
+/*
+ * The logits one row draws from after the penalty, suppression and temperature stages of its flavor (the values the
+ * candidates are ordered by); greedy rows and HARU rows with temperature <= 0 get no temperature. Returns the status
+ * of the stages.
+ */
+int orc_final_logits(const float * logits, int vocab, const spx_row_params * p, const int32_t * hist, int n_hist,
+                     const uint8_t * banned, float * out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

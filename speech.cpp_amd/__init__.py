@@ -1,0 +1,174 @@
+"""Python binding of the gfx950 token sampler's C ABI (include/spx_sampler.h), for tests and bench.py.
+
+The sampler itself is lib/libspx_sampler.so, built from csrc/ by the Makefile beside this file (``make -C
+speech.cpp_amd``). There is no other implementation: when the library is missing this module raises, it never falls
+back to a CPU path.
+
+The row parameters mirror SamplingParams (src/families/qwen3-tts/sampler.h:12-24), haru::Sampling
+(src/families/haru/sampler.h:13-19) and drama3::Sampling (src/families/drama3/sampler.h:12-17), one record per row.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libspx_sampler.so")
+
+F32, BF16 = 0, 1
+TRANSFORMERS, HARU, FISH = 0, 1, 2
+ROW_OK, ROW_REP_PENALTY_OVERFLOW, ROW_TEMPERATURE_OVERFLOW, ROW_NO_FINITE_LOGIT, ROW_NONFINITE_INPUT, \
+    ROW_INVALID_PARAMS = range(6)
+ROW_STATUS_NAMES = ["OK", "REP_PENALTY_OVERFLOW", "TEMPERATURE_OVERFLOW", "NO_FINITE_LOGIT", "NONFINITE_INPUT",
+                    "INVALID_PARAMS"]
+
+# spx_row_params, 32 bytes
+ROW_PARAMS = np.dtype([("flavor", "<i4"), ("greedy", "<i4"), ("temperature", "<f4"), ("top_k", "<i4"),
+                       ("top_p", "<f4"), ("repetition_penalty", "<f4"), ("presence_penalty", "<f4"),
+                       ("frequency_penalty", "<f4")])
+assert ROW_PARAMS.itemsize == 32
+
+# Every symbol include/spx_sampler.h declares.
+EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_last_error",
+           "spx_sampler_last_stats"]
+
+
+class SpxStats(ctypes.Structure):
+    _fields_ = [("rows_fallback", ctypes.c_int32), ("splits", ctypes.c_int32), ("block", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
+
+
+_lib = None
+
+
+def load_library(path=LIB_PATH):
+    """The sampler's shared library with its C signatures declared. Raises when it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"the HIP sampler library is not built: {path} is missing (run make -C {HERE})")
+    lib = ctypes.CDLL(path)
+    p, i32, i64, vp = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
+    lib.spx_sampler_create.argtypes = [ctypes.POINTER(p), i32, i32, i32, i32]
+    lib.spx_sampler_create.restype = i32
+    lib.spx_sampler_destroy.argtypes = [p]
+    lib.spx_sampler_destroy.restype = None
+    lib.spx_sample_rows.argtypes = [p, vp, i32, i32, i32, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.spx_sample_rows.restype = i32
+    lib.spx_argmax_rows.argtypes = [p, vp, i32, i32, i32, i64, vp, i64, vp, vp]
+    lib.spx_argmax_rows.restype = i32
+    lib.spx_last_error.argtypes = []
+    lib.spx_last_error.restype = ctypes.c_char_p
+    lib.spx_sampler_last_stats.argtypes = [p, ctypes.POINTER(SpxStats)]
+    lib.spx_sampler_last_stats.restype = i32
+    _lib = lib
+    return lib
+
+
+def row_params(n, flavor=TRANSFORMERS, greedy=False, temperature=1.0, top_k=0, top_p=1.0, repetition_penalty=1.0,
+               presence_penalty=0.0, frequency_penalty=0.0):
+    """n rows of spx_row_params; each field a scalar or an array of n."""
+    p = np.zeros(n, dtype=ROW_PARAMS)
+    p["flavor"] = flavor
+    p["greedy"] = np.asarray(greedy).astype(np.int32)
+    p["temperature"] = temperature
+    p["top_k"] = top_k
+    p["top_p"] = top_p
+    p["repetition_penalty"] = repetition_penalty
+    p["presence_penalty"] = presence_penalty
+    p["frequency_penalty"] = frequency_penalty
+    return p
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+class SamplerError(RuntimeError):
+    pass
+
+
+class Sampler:
+    """A handle of the sampler on the current device, with its workspace for calls up to the given sizes."""
+
+    def __init__(self, max_rows, max_vocab, max_hist=0, max_out=0):
+        self.lib = load_library()
+        h = ctypes.c_void_p()
+        self._check(self.lib.spx_sampler_create(ctypes.byref(h), max_rows, max_vocab, max_hist, max_out))
+        self.handle = h
+        self.max_out = max_out
+
+    def _check(self, status):
+        if status != 0:
+            raise SamplerError(f"spx status {status}: {self.lib.spx_last_error().decode()}")
+
+    def close(self):
+        if getattr(self, "handle", None):
+            self.lib.spx_sampler_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def sample_rows(self, logits, params, u, hist=None, hist_off=None, banned=None, banned_stride=0, out_ids=None,
+                    out_status=None, out_kept=None, out_cand_ids=None, out_cand_probs=None, stream=None):
+        """Samples every row of `logits` (a 2-D float32 or bfloat16 device tensor, rows may be strided). `params` is a
+        device tensor holding spx_row_params records (see device_params), `u` a float64 device tensor."""
+        import torch
+        rows, vocab = logits.shape
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        ld = logits.stride(0) if rows > 1 else vocab
+        dev = logits.device
+        if out_ids is None:
+            out_ids = torch.empty(rows, dtype=torch.int32, device=dev)
+        if out_status is None:
+            out_status = torch.empty(rows, dtype=torch.int32, device=dev)
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        self._check(self.lib.spx_sample_rows(
+            self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(hist), _ptr(hist_off), _ptr(banned),
+            banned_stride, _ptr(params), _ptr(u), _ptr(out_ids), _ptr(out_status), _ptr(out_kept), _ptr(out_cand_ids),
+            _ptr(out_cand_probs), ctypes.c_void_p(s)))
+        return out_ids, out_status
+
+    def argmax_rows(self, logits, banned=None, banned_stride=0, out_ids=None, stream=None):
+        import torch
+        rows, vocab = logits.shape
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        if out_ids is None:
+            out_ids = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        if logits.stride(1) != 1:
+            raise ValueError("logits rows must be contiguous")
+        ld = logits.stride(0) if rows > 1 else vocab
+        s = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        self._check(self.lib.spx_argmax_rows(self.handle, _ptr(logits), dtype, rows, vocab, ld,
+                                             _ptr(banned), banned_stride, _ptr(out_ids), ctypes.c_void_p(s)))
+        return out_ids
+
+    def last_stats(self):
+        st = SpxStats()
+        self._check(self.lib.spx_sampler_last_stats(self.handle, ctypes.byref(st)))
+        return st
+
+
+def device_params(params, device="cuda"):
+    """spx_row_params records (a numpy array of ROW_PARAMS) as a device tensor."""
+    import torch
+    return torch.from_numpy(np.ascontiguousarray(params).view(np.int32)).to(device)
+
+
+def pack_bans(banned_ids_per_row, vocab):
+    """Suppress masks (uint32 words, bit i%32 of word i/32) from lists of banned ids; one row per list."""
+    words = (vocab + 31) // 32
+    out = np.zeros((len(banned_ids_per_row), words), dtype=np.uint32)
+    for r, ids in enumerate(banned_ids_per_row):
+        ids = np.asarray(ids, dtype=np.int64)
+        ids = ids[(ids >= 0) & (ids < vocab)]
+        np.bitwise_or.at(out[r], ids >> 5, (np.uint32(1) << (ids & 31).astype(np.uint32)))
+    return out

@@ -1,0 +1,262 @@
+// spx_api.cpp — the C ABI of the sampler (include/spx_sampler.h): the handle and its workspace, the checks of each
+// call, the launch shape, and the kernels' LDS layout.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdio>
+#include <cstring>
+#include <string>
+
+#include "../../include/spx_sampler.h"
+#include "spx_internal.h"
+
+struct spx_sampler {
+    int device = 0;
+    int max_rows = 0, max_vocab = 0, max_hist = 0, max_out = 0;
+    int cus = 256;
+    void * ws = nullptr;
+    spx::Launch base{};
+};
+
+namespace {
+
+thread_local std::string g_error;
+
+spx_status fail(spx_status s, const std::string & msg) {
+    g_error = msg;
+    return s;
+}
+
+spx_status hip_fail(hipError_t e, const char * what) {
+    return fail(SPX_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+// The bytes of the LDS region of the special tokens of a chunk of `chunk` tokens.
+size_t bits_bytes(int chunk) { return align_up((size_t) ((chunk + 31) / 32) * 4, 16); }
+
+// Lays out both kernels' LDS and the launch shape for one call.
+void plan_launch(const spx_sampler * s, spx::Launch & a, bool greedy_only, bool has_hist, bool has_ban) {
+    using namespace spx;
+    // Work-groups per row: enough chunks to give the CUs about four work-groups each, but chunks of at least 4096
+    // tokens, and few enough that the last chunk can merge them all.
+    const int max_splits = greedy_only ? kMaxSplitsGreedy : kMaxSplits;
+    int splits = std::max(1, (4 * s->cus + a.rows - 1) / std::max(a.rows, 1));
+    splits = std::min(splits, max_splits);
+    splits = std::min(splits, std::max(1, a.vocab / 4096));
+    int chunk = (a.vocab + splits - 1) / splits;
+    chunk = (int) align_up((size_t) chunk, 64);
+    splits = (a.vocab + chunk - 1) / chunk;
+    a.splits = splits;
+    a.chunk = chunk;
+    a.nwg = a.rows * splits;
+    a.sort_cap = kSortCap;
+    a.slot_cap = has_hist ? s->max_hist : 0;
+
+    size_t off = 0;
+    a.off_red = (int) off;
+    off += 1280;
+    a.off_bits = (int) off;
+    if (has_hist || has_ban) off += bits_bytes(chunk);
+    a.off_slots = (int) off;
+    off += align_up((size_t) a.slot_cap * 12, 16);
+    a.off_cand = (int) off;
+    if (!greedy_only) off += (size_t) kWaves * kCap * 8;
+    a.off_sort = (int) off;
+    if (!greedy_only) off += (size_t) kSortCap * 8;
+    a.lds_bytes = (int) off;
+
+    off = 0;
+    a.fb_off_red = (int) off;
+    off += 1280;
+    a.fb_off_hist = (int) off;
+    off += 3072;
+    a.fb_off_bits = (int) off;
+    if (has_hist || has_ban) off += bits_bytes(a.vocab);
+    a.fb_off_slots = (int) off;
+    off += align_up((size_t) a.slot_cap * 12, 16);
+    a.fb_lds_bytes = (int) off;
+}
+
+spx_status check_common(spx_sampler * s, const void * logits, int dtype, int rows, int vocab, int64_t ld,
+                        const uint32_t * banned, int64_t banned_stride, const int32_t * out_ids) {
+    if (!s) return fail(SPX_ERR_INVALID_ARGUMENT, "null sampler handle");
+    if (rows < 0 || rows > s->max_rows) return fail(SPX_ERR_INVALID_ARGUMENT, "rows outside [0, max_rows]");
+    if (vocab <= 0 || vocab > s->max_vocab) return fail(SPX_ERR_INVALID_ARGUMENT, "vocab outside [1, max_vocab]");
+    if (ld < vocab) return fail(SPX_ERR_INVALID_ARGUMENT, "ld is smaller than vocab");
+    if (dtype != SPX_F32 && dtype != SPX_BF16) return fail(SPX_ERR_INVALID_ARGUMENT, "dtype is neither SPX_F32 nor SPX_BF16");
+    if (rows > 0 && (!logits || !out_ids)) return fail(SPX_ERR_INVALID_ARGUMENT, "null logits or out_ids");
+    if (banned && banned_stride < 0) return fail(SPX_ERR_INVALID_ARGUMENT, "negative banned_stride");
+    if (banned && banned_stride != 0 && banned_stride < (vocab + 31) / 32)
+        return fail(SPX_ERR_INVALID_ARGUMENT, "banned_stride shorter than a mask of vocab bits");
+    return SPX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char * spx_last_error(void) { return g_error.c_str(); }
+
+spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, int max_hist, int max_out) {
+    using namespace spx;
+    if (!out) return fail(SPX_ERR_INVALID_ARGUMENT, "null output pointer");
+    *out = nullptr;
+    if (max_rows <= 0 || max_vocab <= 0 || max_hist < 0 || max_out < 0)
+        return fail(SPX_ERR_INVALID_ARGUMENT, "sizes must be positive");
+    if (max_out > kKeep) return fail(SPX_ERR_INVALID_ARGUMENT, "max_out above 256");
+    auto * s = new spx_sampler();
+    s->max_rows = max_rows;
+    s->max_vocab = max_vocab;
+    s->max_hist = max_hist;
+    s->max_out = max_out;
+    hipError_t e = hipGetDevice(&s->device);
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(e, "hipGetDevice");
+    }
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
+        s->cus = cus;
+    // The LDS a call can ask for: the largest history and the whole vocabulary's bitmap.
+    const size_t slot_bytes = align_up((size_t) max_hist * 12, 16);
+    const size_t stream_max = 1280 + bits_bytes(max_vocab) + slot_bytes + (size_t) kWaves * kCap * 8 + (size_t) kSortCap * 8;
+    const size_t fb_max = 1280 + 3072 + bits_bytes(max_vocab) + slot_bytes;
+    if (stream_max > 160 * 1024 || fb_max > 160 * 1024) {
+        delete s;
+        return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
+    }
+    e = set_lds_limits((int) stream_max, (int) fb_max);
+    if (e != hipSuccess) {
+        delete s;
+        return hip_fail(e, "hipFuncSetAttribute");
+    }
+    // One allocation for the workspace.
+    const size_t n_counters = align_up((size_t) max_rows * 4, 256);
+    const size_t n_partials = align_up((size_t) max_rows * kMaxSplitsGreedy * sizeof(Partial), 256);
+    const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
+    const size_t n_state = align_up((size_t) max_rows * sizeof(RowState), 256);
+    const size_t n_fb = align_up((size_t) (4 + max_rows) * 4, 256);
+    const size_t bytes = n_counters + n_partials + n_cands + n_state + n_fb;
+    e = hipMalloc(&s->ws, bytes);
+    if (e != hipSuccess) {
+        delete s;
+        return e == hipErrorOutOfMemory ? fail(SPX_ERR_OUT_OF_MEMORY, "workspace allocation") : hip_fail(e, "hipMalloc");
+    }
+    e = hipMemset(s->ws, 0, bytes);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void) hipFree(s->ws);
+        delete s;
+        return hip_fail(e, "hipMemset");
+    }
+    char * p = (char *) s->ws;
+    s->base.counters = (uint32_t *) p;
+    p += n_counters;
+    s->base.partials = (Partial *) p;
+    p += n_partials;
+    s->base.part_cands = (uint64_t *) p;
+    p += n_cands;
+    s->base.row_state = (RowState *) p;
+    p += n_state;
+    s->base.fb_count = (int32_t *) p;
+    s->base.fb_rows = (int32_t *) p + 4;
+    s->base.max_hist = max_hist;
+    *out = s;
+    return SPX_OK;
+}
+
+void spx_sampler_destroy(spx_sampler * s) {
+    if (!s) return;
+    if (s->ws) (void) hipFree(s->ws);
+    delete s;
+}
+
+spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
+                           int64_t banned_stride, const spx_row_params * d_params, const double * d_u,
+                           int32_t * d_out_ids, int32_t * d_out_status, int32_t * d_out_kept,
+                           int32_t * d_out_cand_ids, float * d_out_cand_probs, void * stream) {
+    spx_status st = check_common(s, d_logits, dtype, rows, vocab, ld, d_banned, banned_stride, d_out_ids);
+    if (st != SPX_OK) return st;
+    if (rows > 0 && (!d_params || !d_u)) return fail(SPX_ERR_INVALID_ARGUMENT, "null params or u");
+    if ((d_hist == nullptr) != (d_hist_off == nullptr)) return fail(SPX_ERR_INVALID_ARGUMENT, "hist and hist_off go together");
+    if ((d_out_cand_ids == nullptr) != (d_out_cand_probs == nullptr))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "cand_ids and cand_probs go together");
+    if (d_out_cand_ids && s->max_out <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "the handle was created with max_out 0");
+    if (rows == 0) return SPX_OK;
+    spx::Launch a = s->base;
+    a.logits = d_logits;
+    a.ld = ld;
+    a.rows = rows;
+    a.vocab = vocab;
+    a.dtype = dtype;
+    const size_t esz = dtype == SPX_BF16 ? 2 : 4;
+    a.vec_ok = ((uintptr_t) d_logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
+    a.hist = d_hist;
+    a.hist_off = d_hist_off;
+    a.banned = d_banned;
+    a.banned_stride = banned_stride;
+    a.params = d_params;
+    a.u = d_u;
+    a.out_ids = d_out_ids;
+    a.out_status = d_out_status;
+    a.out_kept = d_out_kept;
+    a.out_cand_ids = d_out_cand_ids;
+    a.out_cand_probs = d_out_cand_probs;
+    a.max_out = d_out_cand_ids ? s->max_out : 0;
+    plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
+    hipStream_t hs = (hipStream_t) stream;
+    hipError_t e = spx::launch_stream(a, hs);
+    if (e != hipSuccess) return hip_fail(e, "stream_kernel launch");
+    e = spx::launch_fallback(a, std::min(rows, s->cus), hs);
+    if (e != hipSuccess) return hip_fail(e, "fallback_kernel launch");
+    return SPX_OK;
+}
+
+spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const uint32_t * d_banned, int64_t banned_stride, int32_t * d_out_ids, void * stream) {
+    spx_status st = check_common(s, d_logits, dtype, rows, vocab, ld, d_banned, banned_stride, d_out_ids);
+    if (st != SPX_OK) return st;
+    if (rows == 0) return SPX_OK;
+    spx::Launch a = s->base;
+    a.logits = d_logits;
+    a.ld = ld;
+    a.rows = rows;
+    a.vocab = vocab;
+    a.dtype = dtype;
+    const size_t esz = dtype == SPX_BF16 ? 2 : 4;
+    a.vec_ok = ((uintptr_t) d_logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
+    a.hist = nullptr;
+    a.hist_off = nullptr;
+    a.banned = d_banned;
+    a.banned_stride = banned_stride;
+    a.params = nullptr;
+    a.u = nullptr;
+    a.out_ids = d_out_ids;
+    a.out_status = nullptr;
+    a.out_kept = nullptr;
+    a.out_cand_ids = nullptr;
+    a.out_cand_probs = nullptr;
+    a.max_out = 0;
+    plan_launch(s, a, true, false, d_banned != nullptr);
+    hipError_t e = spx::launch_stream(a, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "stream_kernel launch");
+    return SPX_OK;
+}
+
+spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {
+    if (!s || !out) return fail(SPX_ERR_INVALID_ARGUMENT, "null argument");
+    int32_t c = 0;
+    hipError_t e = hipMemcpy(&c, s->base.fb_count + 2, sizeof(c), hipMemcpyDeviceToHost);
+    if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
+    out->rows_fallback = c;
+    out->splits = 0;
+    out->block = spx::kBlock;
+    out->reserved = 0;
+    return SPX_OK;
+}
+
+}  // extern "C"

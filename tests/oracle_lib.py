@@ -1,0 +1,136 @@
+"""ctypes binding of the oracle (oracle/libspx_oracle.so, the CPU restatement of the reference's samplers) and of
+oracle/_ref/libref_sampling.so (the reference's own src/common/sampling.cpp). Test infrastructure only."""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+ORACLE_DIR = os.path.join(ROOT, "oracle")
+ORACLE_SO = os.path.join(ORACLE_DIR, "libspx_oracle.so")
+REF_SO = os.path.join(ORACLE_DIR, "_ref", "libref_sampling.so")
+
+
+class RowReport(ctypes.Structure):
+    _fields_ = [("id", ctypes.c_int32), ("status", ctypes.c_int32), ("kept", ctypes.c_int32), ("pad", ctypes.c_int32),
+                ("boundary", ctypes.c_double), ("cut", ctypes.c_double)]
+
+
+REPORT = np.dtype([("id", "<i4"), ("status", "<i4"), ("kept", "<i4"), ("pad", "<i4"), ("boundary", "<f8"),
+                   ("cut", "<f8")])
+
+_oracle = None
+_ref = None
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def oracle():
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            subprocess.run(["make", "-C", ORACLE_DIR, "libspx_oracle.so"], check=True, capture_output=True)
+        lib = ctypes.CDLL(ORACLE_SO)
+        vp, i32, i64 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64
+        lib.orc_uniform_fill.argtypes = [ctypes.c_uint64, i32, vp]
+        lib.orc_pick.argtypes = [vp, i32, ctypes.c_double]
+        lib.orc_pick.restype = i32
+        lib.orc_tf_candidates.argtypes = [vp, i32, vp, vp, i32, vp, vp, vp, i32, vp]
+        lib.orc_tf_candidates.restype = i32
+        for f in (lib.orc_haru_candidates, lib.orc_fish_candidates):
+            f.argtypes = [vp, i32, ctypes.c_float, i32, ctypes.c_float, vp, vp, i32, vp]
+            f.restype = i32
+        lib.orc_sample_rows.argtypes = [vp, i32, i32, i32, i64, vp, vp, vp, i64, vp, vp, vp, vp, vp, i32, i32]
+        lib.orc_sample_rows.restype = None
+        lib.orc_final_logits.argtypes = [vp, i32, vp, vp, i32, vp, vp]
+        lib.orc_final_logits.restype = i32
+        _oracle = lib
+    return _oracle
+
+
+def ref():
+    """The reference's own sampling.cpp, or None where the reference checkout was absent when oracle/ was built."""
+    global _ref
+    if _ref is None and os.path.exists(REF_SO):
+        lib = ctypes.CDLL(REF_SO)
+        vp, i32 = ctypes.c_void_p, ctypes.c_int
+        lib.ref_uniform_fill.argtypes = [ctypes.c_uint64, i32, vp]
+        lib.ref_pick.argtypes = [vp, i32, ctypes.c_double]
+        lib.ref_pick.restype = i32
+        lib.ref_temperature_overflow.argtypes = [ctypes.c_float, ctypes.c_char_p, i32, ctypes.c_char_p, i32]
+        lib.ref_temperature_overflow.restype = i32
+        _ref = lib
+    return _ref
+
+
+def uniform_fill(seed, n):
+    out = np.zeros(n, dtype=np.float64)
+    oracle().orc_uniform_fill(seed, n, _ptr(out))
+    return out
+
+
+def ref_uniform_fill(seed, n):
+    out = np.zeros(n, dtype=np.float64)
+    ref().ref_uniform_fill(seed, n, _ptr(out))
+    return out
+
+
+def pick(weights, u):
+    w = np.ascontiguousarray(weights, dtype=np.float64)
+    return oracle().orc_pick(_ptr(w), len(w), u)
+
+
+def _cands(fn, *args, cap):
+    tok = np.zeros(cap, dtype=np.int32)
+    wts = np.zeros(cap, dtype=np.float64)
+    n = ctypes.c_int(0)
+    st = fn(*args, _ptr(tok), _ptr(wts), cap, ctypes.byref(n))
+    return st, tok[:min(n.value, cap)], wts[:min(n.value, cap)]
+
+
+def tf_candidates(logits, params, hist=None, banned=None):
+    """Returns (status, tokens, weights) of the Qwen3-TTS candidates() with the penalty and suppression stages."""
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    p = np.ascontiguousarray(params)
+    h = None if hist is None else np.ascontiguousarray(hist, dtype=np.int32)
+    b = None if banned is None else np.ascontiguousarray(banned, dtype=np.uint8)
+    return _cands(oracle().orc_tf_candidates, _ptr(l), len(l), _ptr(p), _ptr(h), 0 if h is None else len(h), _ptr(b),
+                  cap=len(l))
+
+
+def haru_candidates(logits, temperature, top_k, top_p):
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    return _cands(oracle().orc_haru_candidates, _ptr(l), len(l), temperature, top_k, top_p, cap=len(l))
+
+
+def fish_candidates(logits, temperature, top_k, top_p):
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    return _cands(oracle().orc_fish_candidates, _ptr(l), len(l), temperature, top_k, top_p, cap=len(l))
+
+
+def final_logits(logits, params, hist=None, banned=None):
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    out = np.zeros_like(l)
+    h = None if hist is None else np.ascontiguousarray(hist, dtype=np.int32)
+    b = None if banned is None else np.ascontiguousarray(banned, dtype=np.uint8)
+    st = oracle().orc_final_logits(_ptr(l), len(l), _ptr(np.ascontiguousarray(params)), _ptr(h),
+                                   0 if h is None else len(h), _ptr(b), _ptr(out))
+    return st, out
+
+
+def sample_rows(w, threads=8, cap=0):
+    """The oracle over a tests.workloads.Workload: per-row reports, and the first `cap` candidates and probabilities."""
+    rows, vocab = w["logits"].shape
+    reports = np.zeros(rows, dtype=REPORT)
+    cids = np.zeros((rows, cap), dtype=np.int32) if cap else None
+    cprobs = np.zeros((rows, cap), dtype=np.float64) if cap else None
+    logits = np.ascontiguousarray(w["logits"])
+    dtype = 1 if w["dtype"] == "bf16" else 0
+    oracle().orc_sample_rows(_ptr(logits), dtype, rows, vocab, vocab, _ptr(w["hist"]), _ptr(w["hist_off"]),
+                             _ptr(w["banned"]), w["banned_stride"], _ptr(np.ascontiguousarray(w["params"])),
+                             _ptr(w["u"]), _ptr(reports), _ptr(cids), _ptr(cprobs), cap, threads)
+    return reports, cids, cprobs

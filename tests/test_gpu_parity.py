@@ -1,0 +1,177 @@
+"""Parity of the HIP sampler with the oracle, through the C ABI, on the five workloads and on the edge cases the
+reference's checks exercise (checks/qwen3-tts/qwen3-tts-sampler-check.cpp, qwen3-tts-graph-sampler-check.cpp,
+checks/haru/haru-sampling-check.cpp, checks/drama3/drama3-sampler-check.cpp)."""
+
+import numpy as np
+import pytest
+
+import gpu_harness
+import oracle_lib
+import workloads
+
+pytestmark = pytest.mark.gpu
+
+MAX_OUT = 64
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    spx = workloads.spx_module()
+    return spx.Sampler(max_rows=2048, max_vocab=151936, max_hist=2048, max_out=MAX_OUT)
+
+
+def check(sampler, w, cap=MAX_OUT, allow_explained=True):
+    reports, cids, cprobs = oracle_lib.sample_rows(w, cap=cap)
+    gpu = gpu_harness.run_gpu(sampler, w, max_out=cap)
+    counts, bad = gpu_harness.compare(w, gpu, reports, cids, cprobs)
+    print(w["name"], counts, bad)
+    assert not bad, f"{len(bad)} unexplained rows, first: {bad[:5]}"
+    if not allow_explained:
+        assert counts["tie"] + counts["boundary"] + counts["cut"] == 0
+    return counts, gpu, reports
+
+
+@pytest.mark.parametrize("name,rows", [("talker", 64), ("predictor", 480), ("asr", 64), ("haru", 32), ("mixed", 96)])
+def test_workload_parity(sampler, name, rows):
+    w = workloads.make(name, rows=rows, seed=7)
+    counts, gpu, _ = check(sampler, w)
+    # Explained differences are counted, not hidden: ties dominate the talker rows, whose 8 largest logits are equal.
+    assert counts["same"] + counts["tie"] >= 0.95 * w.rows
+
+
+def test_talker_spikes_are_ties(sampler):
+    # Eight logits at exactly +8: the reference's order among them is libstdc++'s heap order, a pick between them is
+    # an explained tie (checks/qwen3-tts/qwen3-tts-graph-sampler-check.cpp:124-125).
+    w = workloads.make("talker", rows=256, seed=11)
+    check(sampler, w)
+
+
+def test_haru_full_rows(sampler):
+    w = workloads.make("haru", rows=256, seed=3)
+    counts, gpu, reports = check(sampler, w)
+    assert counts["same"] >= 250
+
+
+def test_argmax_rows_banned(sampler):
+    import torch
+    spx = workloads.spx_module()
+    w = workloads.make("asr", rows=64, seed=5)
+    d = gpu_harness.to_device(w)
+    ids = sampler.argmax_rows(d["logits"], banned=d["banned"], banned_stride=0)
+    torch.cuda.synchronize()
+    logits = w["logits"].copy()
+    words = w["banned"][0]
+    i = np.arange(w.vocab)
+    mask = ((words[i >> 5] >> (i & 31).astype(np.uint32)) & 1).astype(bool)
+    logits[:, mask] = -np.inf
+    assert np.array_equal(ids.cpu().numpy(), np.argmax(logits, axis=1))
+
+
+def _one(params_kw, logits, hist=None, banned_ids=None, u=0.5, dtype="f32"):
+    spx = workloads.spx_module()
+    logits = np.atleast_2d(np.asarray(logits, dtype=np.float32))
+    rows, vocab = logits.shape
+    p = spx.row_params(rows, **params_kw)
+    h, off = (None, None)
+    if hist is not None:
+        h, off = workloads.csr([hist] * rows)
+    banned = spx.pack_bans([banned_ids] * 1, vocab) if banned_ids is not None else None
+    if dtype == "bf16":
+        logits = workloads.to_bf16_bits(logits)
+    return workloads.Workload(name="edge", logits=logits, dtype=dtype, params=p, u=np.full(rows, u), hist=h,
+                              hist_off=off, banned=banned, banned_stride=0)
+
+
+EDGE = [
+    ("penalty 1e-40 greedy", dict(greedy=True, repetition_penalty=1e-40), [1.0, 2.0], [0, 1]),
+    ("penalty 1e-40 draw", dict(repetition_penalty=1e-40), [1.0, 2.0], [0, 1]),
+    ("temperature 1e-38", dict(temperature=1e-38, top_k=50), np.linspace(-3, 10, 300), None),
+    ("all equal", dict(temperature=0.8, top_k=0, top_p=0.9), np.zeros(1000), None),
+    ("all equal top-k", dict(temperature=0.8, top_k=7), np.zeros(1000), None),
+    ("single token", dict(temperature=0.8), [0.3], None),
+    ("two tokens", dict(temperature=0.8, top_p=0.5), [0.3, 0.1], None),
+    ("vocab 5", dict(temperature=1.0, top_k=3), [0.1, 0.5, -1.0, 2.0, 0.7], None),
+    ("nan first", dict(greedy=True), [np.nan, 1.0, 2.0], None),
+    ("nan later greedy", dict(greedy=True), [1.0, np.nan, 2.0, 2.0], None),
+    ("nan later draw", dict(temperature=1.0), [1.0, np.nan, 2.0], None),
+    ("+inf", dict(temperature=1.0), [1.0, np.inf, 2.0], None),
+    ("+inf penalty", dict(temperature=1.0, repetition_penalty=1.1), [1.0, np.inf, 2.0], [2]),
+    ("-inf all", dict(temperature=1.0), [-np.inf] * 10, None),
+    ("haru all -inf", dict(flavor=1, temperature=0.7, top_k=3), [-np.inf] * 10, None),
+    ("haru nan", dict(flavor=1, temperature=0.7), [1.0, np.nan], None),
+    ("haru -inf ok", dict(flavor=1, temperature=0.7, top_k=0), [1.0, -np.inf, 0.5], None),
+    ("haru greedy T0", dict(flavor=1, temperature=0.0), [1.0, 3.0, 3.0], None),
+    ("haru tiny T", dict(flavor=1, temperature=1e-38, top_k=5), [1.0, 2.0, -3.0], None),
+    ("fish -inf", dict(flavor=2, temperature=1.0, top_k=3), [1.0, -np.inf, 0.5], None),
+    ("fish T0", dict(flavor=2, temperature=0.0, top_k=3, top_p=0.9), [1.0, 1.0 + 1e-6, 0.5], None),
+    ("fish top-k 0", dict(flavor=2, temperature=1.0, top_k=0, top_p=0.9), np.linspace(0, 1, 64), None),
+    ("negative logits penalty", dict(temperature=1.0, repetition_penalty=1.3), [-1.0, -2.0, 0.5, 3.0], [0, 0, 1, 3, 9, -4]),
+    ("presence frequency", dict(temperature=1.0, presence_penalty=0.5, frequency_penalty=0.25), [1.0, 2.0, 3.0, 0.0],
+     [2, 2, 2, 1]),
+    ("top-p 0", dict(temperature=0.9, top_p=0.0), np.linspace(-1, 1, 50), None),
+    ("top-k beyond vocab", dict(temperature=1.1, top_k=5000), np.random.default_rng(0).normal(0, 2, 2048), None),
+    ("top-k 300 fallback", dict(temperature=1.0, top_k=300), np.random.default_rng(1).normal(0, 1, 4096), None),
+    ("haru top-k 1000", dict(flavor=1, temperature=1.2, top_k=1000, top_p=0.9), np.random.default_rng(2).normal(0, 2, 8192), None),
+    ("wide top-p fallback", dict(temperature=2.5, top_k=0, top_p=0.99), np.random.default_rng(3).normal(0, 2, 3072), None),
+    ("full draw fallback", dict(temperature=3.0, top_k=0, top_p=1.0), np.random.default_rng(4).normal(0, 1, 20000), None),
+    ("invalid flavor", dict(flavor=7), [1.0, 2.0], None),
+    ("invalid temperature", dict(temperature=0.0), [1.0, 2.0], None),
+]
+
+
+@pytest.mark.parametrize("name,kw,logits,hist", EDGE, ids=[e[0] for e in EDGE])
+@pytest.mark.parametrize("u", [0.0, 0.37, 0.999, 1.0])
+def test_edge(sampler, name, kw, logits, hist, u):
+    w = _one(kw, logits, hist=hist, u=u)
+    check(sampler, w)
+
+
+def test_banned_per_row_bf16(sampler):
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(9)
+    rows, vocab = 16, 5003  # a vocabulary that leaves the rows unaligned
+    logits = rng.normal(0, 2, (rows, vocab)).astype(np.float32)
+    banned = spx.pack_bans([rng.choice(vocab, 40 + r, replace=False) for r in range(rows)], vocab)
+    p = spx.row_params(rows, temperature=0.8, top_k=np.array([0, 5, 50, 0] * 4), top_p=0.95)
+    w = workloads.Workload(name="bans", logits=workloads.to_bf16_bits(logits), dtype="bf16", params=p,
+                           u=workloads.uniforms(5, rows), hist=None, hist_off=None, banned=banned,
+                           banned_stride=banned.shape[1])
+    check(sampler, w)
+
+
+def test_flavors_mixed_batch(sampler):
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(12)
+    rows, vocab = 60, 4097  # Drama 3's main-token vocabulary
+    logits = rng.normal(0, 3, (rows, vocab)).astype(np.float32)
+    flavor = np.array([0, 1, 2] * 20)
+    p = spx.row_params(rows, flavor=flavor, temperature=rng.uniform(0.3, 1.5, rows).astype(np.float32),
+                       top_k=rng.choice([0, 1, 25, 30, 200], rows), top_p=rng.uniform(0.5, 1.0, rows).astype(np.float32))
+    hist, off = workloads.csr([rng.integers(-5, vocab + 5, 40) for _ in range(rows)])
+    p["repetition_penalty"][flavor == 0] = 1.2
+    w = workloads.Workload(name="flavors", logits=logits, dtype="f32", params=p, u=workloads.uniforms(8, rows),
+                           hist=hist, hist_off=off, banned=None, banned_stride=0)
+    check(sampler, w)
+
+
+def test_repeated_calls_reuse_workspace(sampler):
+    # The per-row counters and the fallback list reset themselves: calls in a row give the same answers.
+    w = workloads.make("mixed", rows=64, seed=21)
+    reports, _, _ = oracle_lib.sample_rows(w)
+    d = gpu_harness.to_device(w)
+    first = gpu_harness.run_gpu(sampler, w, d)
+    for _ in range(3):
+        again = gpu_harness.run_gpu(sampler, w, d)
+        assert np.array_equal(first["ids"], again["ids"])
+        assert np.array_equal(first["status"], again["status"])
+
+
+def test_empty_batch(sampler):
+    import torch
+    spx = workloads.spx_module()
+    logits = torch.zeros((0, 100), device="cuda")
+    p = spx.device_params(spx.row_params(0))
+    u = torch.zeros(0, dtype=torch.float64, device="cuda")
+    ids, st = sampler.sample_rows(logits, p, u)
+    torch.cuda.synchronize()
+    assert ids.numel() == 0
