@@ -1,0 +1,180 @@
+"""Benchmark of the gfx950 token sampler on its headline workload.
+
+A step is one spx_sample_rows call over one batch: 256 rows x 151936 fp32 logits with a Zipf-shaped profile, a 1024-id
+history per row under repetition 1.1 and presence 0.5, temperature 0.7, top-k off, top-p 0.9, one uniform per row
+(the Haru-4B-style text-sampling workload). Inputs are synthetic, seeded, and resident in HBM before timing starts.
+
+Prints one JSON line: rows/s over the timed steps (whole job), the roofline of the sampling kernel (algorithmic
+bytes per launch over its average launch time, from HIP events recorded on the launch stream), and the CPU baseline:
+the oracle (a C++ restatement of the reference's sampler) timed on a bounded sample of the same rows on this host.
+
+usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload haru] [--cpu-rows 48] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "tests"))
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
+WORKLOAD_LABELS = {
+    "haru": "Haru-4B-style text sampling: 256 x 151936 fp32, hist 1024, rep 1.1 + presence 0.5, T 0.7, top-p 0.9",
+    "asr": "Qwen3-ASR-style greedy: 64 x 151936 fp32, 300 banned ids, argmax",
+    "mixed": "heterogeneous mixed batch: 2048 x 151936 bf16, per-row T/top-k/top-p, hist U[0,2048], 1% greedy",
+    "predictor": "Qwen3-TTS code-predictor batch: 480 x 2048 fp32, hist 64, rep 1.05, T 0.9, top-k 50",
+    "talker": "Qwen3-TTS talker step: 1 x 3072 fp32, hist 128, rep 1.05, T 0.9, top-k 50",
+}
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="haru", choices=sorted(WORKLOAD_LABELS))
+    ap.add_argument("--cpu-rows", type=int, default=48)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--seed", type=int, default=1234)
+    return ap.parse_args()
+
+
+def cpu_baseline(w, rows, threads_list):
+    """The oracle on the first `rows` rows, median of 5 timed runs after one warm-up, per thread count."""
+    import oracle_lib
+    sub = dict(w)
+    sub["logits"] = w["logits"][:rows]
+    sub["params"] = w["params"][:rows]
+    sub["u"] = w["u"][:rows]
+    if w["hist"] is not None:
+        sub["hist_off"] = w["hist_off"][:rows + 1]
+        sub["hist"] = w["hist"][:int(w["hist_off"][rows])]
+    sub = type(w)(sub)
+    out = {}
+    for t in threads_list:
+        oracle_lib.sample_rows(sub, threads=t)
+        times = []
+        for _ in range(5):
+            t0 = time.perf_counter()
+            oracle_lib.sample_rows(sub, threads=t)
+            times.append(time.perf_counter() - t0)
+        out[t] = rows / statistics.median(times)
+    return out
+
+
+def host_cores():
+    n = os.cpu_count() or 1
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    share = int(os.environ.get("OMP_NUM_THREADS", n))
+    return max(1, min(n, share))
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
+              "rows shard across GPUs with no exchange, so the N-GPU rate is N times the one-GPU rate.",
+              file=sys.stderr)
+        sys.exit(2)
+    import torch
+    import gpu_harness
+    import workloads
+
+    spx = workloads.spx_module()
+    w = workloads.make(args.workload, seed=args.seed)
+    rows, vocab = w.rows, w.vocab
+    max_hist = int(np.max(np.diff(w["hist_off"]))) if w["hist"] is not None else 0
+    d = gpu_harness.to_device(w)
+    sampler = spx.Sampler(max_rows=rows, max_vocab=vocab, max_hist=max_hist, max_out=0)
+    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    status = torch.empty(rows, dtype=torch.int32, device="cuda")
+    stream = torch.cuda.current_stream()
+
+    def step():
+        sampler.sample_rows(d["logits"], d["params"], d["u"], hist=d["hist"], hist_off=d["hist_off"],
+                            banned=d["banned"], banned_stride=w["banned_stride"], out_ids=ids, out_status=status,
+                            stream=stream.cuda_stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    fb_before = sampler.last_stats().rows_fallback
+
+    # The timed region: K steps bracketed by synchronizations; an event pair around every launch, on its stream.
+    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    ends = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        starts[i].record(stream)
+        step()
+        ends[i].record(stream)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    launch_ms = statistics.mean(s.elapsed_time(e) for s, e in zip(starts, ends))
+    fb_rows = (sampler.last_stats().rows_fallback - fb_before) / max(args.steps, 1)
+    bad = int((status.cpu().numpy() != 0).sum())
+
+    algo_bytes = workloads.algorithmic_bytes(w)
+    achieved = algo_bytes / (launch_ms * 1e-3) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic.json")
+    if os.path.exists(tpath):
+        t = json.load(open(tpath)).get(args.workload)
+        if t:
+            traffic = t.get("hbm_bytes_per_launch")
+
+    value = rows * args.steps / elapsed
+    line = {
+        "metric": "sampled rows/sec + achieved HBM GB/s at 256x151936 fp32 top-p, 1 MI355X",
+        "value": value,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": elapsed * 1e3 / args.steps,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32" if w["dtype"] == "f32" else "bf16",
+        "data": "synthetic (seeded Zipf-profile logits, random histories, MT19937-64 uniforms)",
+        "config": {"workload": WORKLOAD_LABELS[args.workload], "rows": rows, "vocab": vocab,
+                   "rows_multi_pass_per_step": fb_rows, "rows_refused": bad},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": algo_bytes, "launch_ms": launch_ms},
+    }
+    if not args.no_cpu:
+        cores = host_cores()
+        n = min(args.cpu_rows, rows)
+        rates = cpu_baseline(w, n, sorted({1, cores}))
+        line["cpu_baseline"] = {"value": rates[cores], "unit": "rows/s", "cores": cores, "kind": "port",
+                                "sample": f"the first {n} rows of the same batch, oracle restatement of the reference "
+                                          f"sampler, median of 5 runs, std::thread over {cores} threads "
+                                          f"({cpu_model()})",
+                                "value_1core": rates[1]}
+        line["vs_cpu"] = value / rates[cores]
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

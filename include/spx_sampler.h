@@ -131,10 +131,10 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
 /* Message of the last failed call on this thread ("" when none). */
 const char * spx_last_error(void);
 
-/* Diagnostics of the last call on a handle (host-side copy, valid after the stream has synchronized). */
+/* Diagnostics of a handle (a host-side copy; synchronizes with the device). */
 typedef struct spx_stats {
-    int32_t rows_fallback; /* rows whose candidate set needed the multi-pass path */
-    int32_t splits;        /* work-groups per row of the streaming pass */
+    int32_t rows_fallback; /* rows resolved by the multi-pass path since the handle was created */
+    int32_t splits;        /* reserved */
     int32_t block;         /* threads per work-group */
     int32_t reserved;
 } spx_stats;

@@ -110,6 +110,9 @@ bool valid_params(const spx_row_params & p, bool has_ban) {
     }
     if (p.flavor == SPX_FLAVOR_FISH && has_ban) return false;
     if (p.flavor == SPX_FLAVOR_TRANSFORMERS && !p.greedy && !(p.temperature > 0.0f)) return false;
+    // A temperature that rounds to infinity, which the reference's engines refuse before sampling
+    // (src/engines/qwen3-tts-engine.cpp:47-56).
+    if (!p.greedy && p.temperature == INFINITY) return false;
     return true;
 }
 

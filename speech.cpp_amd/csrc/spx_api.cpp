@@ -34,8 +34,11 @@ spx_status hip_fail(hipError_t e, const char * what) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// The bytes of the LDS region of the special tokens of a chunk of `chunk` tokens.
-size_t bits_bytes(int chunk) { return align_up((size_t) ((chunk + 31) / 32) * 4, 16); }
+// The bytes of the LDS regions of the special tokens of a chunk of `chunk` tokens: two bit words and a rank per 32.
+size_t bits_bytes(int chunk) {
+    const size_t words = (size_t) (chunk + 31) / 32;
+    return align_up(words * 8, 16) + align_up(words * 4, 16);
+}
 
 // Lays out both kernels' LDS and the launch shape for one call.
 void plan_launch(const spx_sampler * s, spx::Launch & a, bool greedy_only, bool has_hist, bool has_ban) {
@@ -58,8 +61,11 @@ void plan_launch(const spx_sampler * s, spx::Launch & a, bool greedy_only, bool 
     size_t off = 0;
     a.off_red = (int) off;
     off += 1280;
+    const size_t words = (size_t) (chunk + 31) / 32;
     a.off_bits = (int) off;
-    if (has_hist || has_ban) off += bits_bytes(chunk);
+    if (has_hist || has_ban) off += align_up(words * 8, 16);
+    a.off_rank = (int) off;
+    if (has_hist || has_ban) off += align_up(words * 4, 16);
     a.off_slots = (int) off;
     off += align_up((size_t) a.slot_cap * 12, 16);
     a.off_cand = (int) off;
@@ -67,17 +73,6 @@ void plan_launch(const spx_sampler * s, spx::Launch & a, bool greedy_only, bool 
     a.off_sort = (int) off;
     if (!greedy_only) off += (size_t) kSortCap * 8;
     a.lds_bytes = (int) off;
-
-    off = 0;
-    a.fb_off_red = (int) off;
-    off += 1280;
-    a.fb_off_hist = (int) off;
-    off += 3072;
-    a.fb_off_bits = (int) off;
-    if (has_hist || has_ban) off += bits_bytes(a.vocab);
-    a.fb_off_slots = (int) off;
-    off += align_up((size_t) a.slot_cap * 12, 16);
-    a.fb_lds_bytes = (int) off;
 }
 
 spx_status check_common(spx_sampler * s, const void * logits, int dtype, int rows, int vocab, int64_t ld,
@@ -120,15 +115,14 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
         s->cus = cus;
-    // The LDS a call can ask for: the largest history and the whole vocabulary's bitmap.
+    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary.
     const size_t slot_bytes = align_up((size_t) max_hist * 12, 16);
-    const size_t stream_max = 1280 + bits_bytes(max_vocab) + slot_bytes + (size_t) kWaves * kCap * 8 + (size_t) kSortCap * 8;
-    const size_t fb_max = 1280 + 3072 + bits_bytes(max_vocab) + slot_bytes;
-    if (stream_max > 160 * 1024 || fb_max > 160 * 1024) {
+    const size_t lds_max = 1280 + bits_bytes(max_vocab) + slot_bytes + (size_t) kWaves * kCap * 8 + (size_t) kSortCap * 8;
+    if (lds_max > 160 * 1024) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
     }
-    e = set_lds_limits((int) stream_max, (int) fb_max);
+    e = set_lds_limits((int) lds_max);
     if (e != hipSuccess) {
         delete s;
         return hip_fail(e, "hipFuncSetAttribute");
@@ -137,9 +131,8 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     const size_t n_counters = align_up((size_t) max_rows * 4, 256);
     const size_t n_partials = align_up((size_t) max_rows * kMaxSplitsGreedy * sizeof(Partial), 256);
     const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
-    const size_t n_state = align_up((size_t) max_rows * sizeof(RowState), 256);
-    const size_t n_fb = align_up((size_t) (4 + max_rows) * 4, 256);
-    const size_t bytes = n_counters + n_partials + n_cands + n_state + n_fb;
+    const size_t n_fb = 256;
+    const size_t bytes = n_counters + n_partials + n_cands + n_fb;
     e = hipMalloc(&s->ws, bytes);
     if (e != hipSuccess) {
         delete s;
@@ -159,10 +152,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     p += n_partials;
     s->base.part_cands = (uint64_t *) p;
     p += n_cands;
-    s->base.row_state = (RowState *) p;
-    p += n_state;
     s->base.fb_count = (int32_t *) p;
-    s->base.fb_rows = (int32_t *) p + 4;
     s->base.max_hist = max_hist;
     *out = s;
     return SPX_OK;
@@ -208,11 +198,8 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_cand_probs = d_out_cand_probs;
     a.max_out = d_out_cand_ids ? s->max_out : 0;
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
-    hipStream_t hs = (hipStream_t) stream;
-    hipError_t e = spx::launch_stream(a, hs);
+    hipError_t e = spx::launch_stream(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "stream_kernel launch");
-    e = spx::launch_fallback(a, std::min(rows, s->cus), hs);
-    if (e != hipSuccess) return hip_fail(e, "fallback_kernel launch");
     return SPX_OK;
 }
 
@@ -250,7 +237,7 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {
     if (!s || !out) return fail(SPX_ERR_INVALID_ARGUMENT, "null argument");
     int32_t c = 0;
-    hipError_t e = hipMemcpy(&c, s->base.fb_count + 2, sizeof(c), hipMemcpyDeviceToHost);
+    hipError_t e = hipMemcpy(&c, s->base.fb_count, sizeof(c), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
     out->rows_fallback = c;
     out->splits = 0;

@@ -58,38 +58,62 @@ __device__ __forceinline__ T wave_shfl_xor(T v, int mask) {
     return __shfl_xor(v, mask, kWave);
 }
 
+// Wave reductions through DPP: within each row of 16 lanes a quad swap, a pair swap and two rotations leave every
+// lane with its row's result; the four rows are then combined from one lane each. Every lane must be active.
+template <int CTRL>
+__device__ __forceinline__ uint32_t dpp_u32(uint32_t v) {
+    return (uint32_t) __builtin_amdgcn_update_dpp(0, (int) v, CTRL, 0xf, 0xf, false);
+}
+__device__ __forceinline__ uint32_t lane_u32(uint32_t v, int l) { return (uint32_t) __builtin_amdgcn_readlane((int) v, l); }
+
+template <typename Op>
+__device__ __forceinline__ uint32_t wave_reduce_u32(uint32_t v, Op op) {
+    v = op(v, dpp_u32<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = op(v, dpp_u32<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = op(v, dpp_u32<0x124>(v));  // row_ror:4
+    v = op(v, dpp_u32<0x128>(v));  // row_ror:8
+    return op(op(lane_u32(v, 0), lane_u32(v, 16)), op(lane_u32(v, 32), lane_u32(v, 48)));
+}
+template <typename Op>
+__device__ __forceinline__ uint64_t wave_reduce_u64(uint64_t v, Op op) {
+    auto step = [&](uint64_t a, uint32_t lo, uint32_t hi) { return op(a, ((uint64_t) hi << 32) | lo); };
+    v = step(v, dpp_u32<0xB1>((uint32_t) v), dpp_u32<0xB1>((uint32_t) (v >> 32)));
+    v = step(v, dpp_u32<0x4E>((uint32_t) v), dpp_u32<0x4E>((uint32_t) (v >> 32)));
+    v = step(v, dpp_u32<0x124>((uint32_t) v), dpp_u32<0x124>((uint32_t) (v >> 32)));
+    v = step(v, dpp_u32<0x128>((uint32_t) v), dpp_u32<0x128>((uint32_t) (v >> 32)));
+    auto at = [&](int l) { return ((uint64_t) lane_u32((uint32_t) (v >> 32), l) << 32) | lane_u32((uint32_t) v, l); };
+    return op(op(at(0), at(16)), op(at(32), at(48)));
+}
+
 __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(v, m, kWave);
-        v = o > v ? o : v;
-    }
-    return v;
+    return wave_reduce_u64(v, [](uint64_t a, uint64_t b) { return a > b ? a : b; });
 }
 __device__ __forceinline__ uint64_t wave_min_u64(uint64_t v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint64_t o = __shfl_xor(v, m, kWave);
-        v = o < v ? o : v;
-    }
-    return v;
+    return wave_reduce_u64(v, [](uint64_t a, uint64_t b) { return a < b ? a : b; });
 }
 __device__ __forceinline__ uint32_t wave_max_u32(uint32_t v) {
-    for (int m = 32; m >= 1; m >>= 1) {
-        const uint32_t o = __shfl_xor(v, m, kWave);
-        v = o > v ? o : v;
-    }
-    return v;
+    return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
+    return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
 }
 __device__ __forceinline__ int wave_sum_i32(int v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
+    return (int) wave_reduce_u32((uint32_t) v, [](uint32_t a, uint32_t b) { return a + b; });
 }
 __device__ __forceinline__ uint32_t wave_or_u32(uint32_t v) {
-    for (int m = 32; m >= 1; m >>= 1) v |= __shfl_xor(v, m, kWave);
-    return v;
+    return wave_reduce_u32(v, [](uint32_t a, uint32_t b) { return a | b; });
+}
+// The largest of the lanes' floats (no NaN among them).
+__device__ __forceinline__ float wave_max_f32(float v) {
+    return __uint_as_float(wave_reduce_u32(__float_as_uint(v), [](uint32_t a, uint32_t b) {
+        return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+    }));
 }
 __device__ __forceinline__ double wave_sum_f64(double v) {
-    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, kWave);
-    return v;
+    const uint64_t r = wave_reduce_u64((uint64_t) __double_as_longlong(v), [](uint64_t a, uint64_t b) {
+        return (uint64_t) __double_as_longlong(__longlong_as_double((long long) a) + __longlong_as_double((long long) b));
+    });
+    return __longlong_as_double((long long) r);
 }
 
 // Inclusive prefix sum over the wave's lanes (Hillis-Steele with shuffles).

@@ -8,13 +8,14 @@
 
 namespace spx {
 
-// Threads per work-group of the streaming pass, and of the multi-pass path.
+// Threads per work-group.
 constexpr int kBlock = 256;
-constexpr int kFbBlock = 1024;
 constexpr int kWaves = kBlock / 64;
 // Entries a wave keeps: the top-k of a row with top_k <= kKeep, and the top kKeep of a row drawing over more
 // (its top-p set must end within them, or the row takes the multi-pass path).
 constexpr int kKeep = 256;
+// Entries a wave keeps for a row drawing over more than kKeep tokens.
+constexpr int kKeepFull = 128;
 // A wave's buffer: its kKeep best plus one offer of 64 lanes x 4 elements before it must compact.
 constexpr int kCap = 512;
 constexpr int kPerLane = kCap / 64;
@@ -25,24 +26,15 @@ constexpr int kSortCap = 1024;  // >= kWaves * kKeep and >= kMaxSplits * kKeep, 
 
 // What a chunk of a row leaves for the last chunk of its row.
 struct Partial {
-    uint64_t best;  // greedy: the largest entry of the final logits
-    uint64_t low;   // the last token of the order
-    double s;       // sum of exp(q - m)
+    uint64_t best;     // greedy: the largest entry of the final logits (0: none)
+    uint64_t low;      // the last token of the order
+    double s;          // sum of exp(q - m)
     float m;
+    float mx, mn;      // range of the final logits
     uint32_t flags;
-    int32_t n;      // sorted entries published
+    int32_t n;         // sorted entries published
     int32_t complete;  // 1 when the chunk's every valid token is among them
-    uint64_t kth;   // its K-th entry (0 when it holds fewer than K)
-};
-
-// What the multi-pass path needs of a row the one-pass path could not finish.
-struct RowState {
-    double s;
-    float m;
-    float top;
-    uint64_t low;
-    uint32_t flags;
-    int32_t pad;
+    uint64_t kth;      // its K-th entry (0 when it holds fewer than K)
 };
 
 struct Launch {
@@ -65,17 +57,13 @@ struct Launch {
     int max_out;
     int splits, chunk, nwg;
     int sort_cap;
-    // LDS layout of stream_kernel (byte offsets)
-    int off_bits, off_slots, off_cand, off_sort, off_red, lds_bytes;
-    // LDS layout of fallback_kernel
-    int fb_off_bits, fb_off_slots, fb_off_hist, fb_off_red, fb_lds_bytes;
+    // LDS layout (byte offsets). The multi-pass path keeps its radix histograms in the sort region.
+    int off_bits, off_rank, off_slots, off_cand, off_sort, off_red, lds_bytes;
     // workspace
     uint32_t * counters;   // [max_rows], each back to 0 after its row's last chunk
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]
     uint64_t * part_cands; // [max_rows * kMaxSplits * kKeep]
-    RowState * row_state;  // [max_rows]
-    int32_t * fb_count;    // [3]: rows listed, work-groups done, rows listed by the last call
-    int32_t * fb_rows;     // [max_rows]
+    int32_t * fb_count;    // rows the multi-pass path has resolved since the handle was made
 };
 
 }  // namespace spx
@@ -84,6 +72,5 @@ struct Launch {
 
 namespace spx {
 hipError_t launch_stream(const Launch & a, hipStream_t s);
-hipError_t launch_fallback(const Launch & a, int grid, hipStream_t s);
-hipError_t set_lds_limits(int stream_bytes, int fb_bytes);
+hipError_t set_lds_limits(int stream_bytes);
 }  // namespace spx

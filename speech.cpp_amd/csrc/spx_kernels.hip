@@ -12,8 +12,8 @@
 //     wave's exact top K, so the union over waves holds the row's top K without a sort of the row.
 // The last work-group of a row (an atomic counter per row, reset by that work-group) merges the chunks' partial
 // results, sorts the few hundred surviving entries in LDS and applies the flavor's rule: softmax weights in double,
-// the top-p cut, and pick() with the row's uniform. A row whose top-p set runs beyond the entries kept goes on a list
-// for fallback_kernel, which resolves it exactly with radix selects over (count, mass) histograms.
+// the top-p cut, and pick() with the row's uniform. A row whose top-p set runs beyond the entries kept is resolved
+// by that same work-group with radix selects over (count, mass) histograms of the whole row.
 //
 // Citations are relative to the reference checkout (nyosegawa/speech.cpp 0.11.1).
 
@@ -35,11 +35,8 @@ enum Mode : int { kGreedy = 0, kTopK = 1, kFull = 2, kInvalid = 3 };
 
 enum Flag : uint32_t {
     kNaN = 1u,        // a NaN among the final logits
-    kPosInf = 2u,     // +inf among the final logits
-    kFinite = 4u,     // a finite final logit
     kTempOver = 8u,   // HARU: a finite logit whose quotient is not finite (src/families/haru/sampler.cpp:34)
-    kNaN0 = 16u,      // the logit of token 0 is NaN (std::max_element then answers 0)
-    kNegInf = 32u,    // -inf among the final logits (banned tokens included)
+    kNaN0 = 16u,      // the final logit of token 0 is NaN (std::max_element then answers 0)
     kBadHist = 64u,   // the row's history is longer than the handle was created for
 };
 
@@ -79,6 +76,9 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
           __builtin_isnan(p.frequency_penalty);
     bad = bad || (p.flavor == SPX_FLAVOR_FISH && has_ban);
     bad = bad || (p.flavor == SPX_FLAVOR_TRANSFORMERS && !p.greedy && !(p.temperature > 0.0f));
+    // a temperature the float rounds to infinity, which the reference's engines refuse
+    // (src/engines/qwen3-tts-engine.cpp:47-56)
+    bad = bad || (!p.greedy && p.temperature == INFINITY);
     if (bad) {
         pl.mode = kInvalid;
         return pl;
@@ -99,7 +99,7 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
         pl.kc = k;
     } else {
         pl.mode = kFull;
-        pl.kc = kKeep;
+        pl.kc = kKeepFull;
     }
     pl.need_s = pl.mode == kFull || p.flavor == SPX_FLAVOR_FISH;
     // The last token of a draw over every token: pick() returns it where u passes every cumulative share.
@@ -200,7 +200,11 @@ __device__ inline void block_sort_desc(uint64_t * a, int n) {
 // The wave's candidate buffer
 // ------------------------------------------------------------------------------------------------------------------
 
-// The K-th largest entry of the n entries the wave holds in v[] (kPerLane per lane, 0 for none), 1 <= K <= n.
+// Number of set predicates over the wave.
+__device__ __forceinline__ int wave_count(bool p) { return (int) __popcll(ballot(p)); }
+
+// The K-th largest entry of the n entries the wave holds in v[] (kPerLane per lane, 0 for none), 1 <= K <= n. The
+// counts of each step are ballots, so the search stays in scalar registers.
 __device__ __forceinline__ uint64_t wave_kth_largest(const uint64_t (&v)[kPerLane], int K) {
     // First the K-th largest key (the high word), by a bitwise search from the highest bit where keys differ.
     uint32_t hi = 0, lo = 0xffffffffu;
@@ -212,8 +216,8 @@ __device__ __forceinline__ uint64_t wave_kth_largest(const uint64_t (&v)[kPerLan
         }
     }
     hi = wave_max_u32(hi);
-    lo = ~wave_max_u32(~lo);
-    uint32_t key = 0;
+    lo = wave_min_u32(lo);
+    uint32_t key = hi;
     if (hi != lo) {
         const int top = 31 - __builtin_clz(hi ^ lo);
         key = hi & ~((top == 31) ? 0xffffffffu : ((2u << top) - 1u));
@@ -221,21 +225,17 @@ __device__ __forceinline__ uint64_t wave_kth_largest(const uint64_t (&v)[kPerLan
             const uint32_t c = key | (1u << b);
             int cnt = 0;
 #pragma unroll
-            for (int j = 0; j < kPerLane; j++) cnt += (v[j] != 0 && entry_key(v[j]) >= c) ? 1 : 0;
-            if (wave_sum_i32(cnt) >= K) key = c;
+            for (int j = 0; j < kPerLane; j++) cnt += wave_count(v[j] != 0 && entry_key(v[j]) >= c);
+            if (cnt >= K) key = c;
         }
-    } else {
-        key = hi;
     }
     // Entries above that key, and the ties at it.
     int gt = 0, eq = 0;
 #pragma unroll
     for (int j = 0; j < kPerLane; j++) {
-        gt += (v[j] != 0 && entry_key(v[j]) > key) ? 1 : 0;
-        eq += (v[j] != 0 && entry_key(v[j]) == key) ? 1 : 0;
+        gt += wave_count(v[j] != 0 && entry_key(v[j]) > key);
+        eq += wave_count(v[j] != 0 && entry_key(v[j]) == key);
     }
-    gt = wave_sum_i32(gt);
-    eq = wave_sum_i32(eq);
     const int need = K - gt;  // 1 <= need <= eq
     // Among the ties, the need-th largest low word (the lowest ids come first).
     uint32_t lw;
@@ -245,28 +245,30 @@ __device__ __forceinline__ uint64_t wave_kth_largest(const uint64_t (&v)[kPerLan
         for (int j = 0; j < kPerLane; j++) {
             if (v[j] != 0 && entry_key(v[j]) == key) m = min(m, (uint32_t) v[j]);
         }
-        lw = ~wave_max_u32(~m);
+        lw = wave_min_u32(m);
     } else {
         lw = 0;
         for (int b = 31; b >= 0; b--) {
             const uint32_t c = lw | (1u << b);
             int cnt = 0;
 #pragma unroll
-            for (int j = 0; j < kPerLane; j++) cnt += (v[j] != 0 && entry_key(v[j]) == key && (uint32_t) v[j] >= c) ? 1 : 0;
-            if (wave_sum_i32(cnt) >= need) lw = c;
+            for (int j = 0; j < kPerLane; j++) cnt += wave_count(v[j] != 0 && entry_key(v[j]) == key && (uint32_t) v[j] >= c);
+            if (cnt >= need) lw = c;
         }
     }
     return ((uint64_t) key << 32) | lw;
 }
 
-// Keeps the wave's top K of its n entries (exactly K), in buf[0..K); returns the K-th, the new threshold.
-__device__ __forceinline__ uint64_t wave_compact(uint64_t * buf, int & n, int K) {
+// Keeps the wave's top K of its n entries (exactly K), in buf[0..K); returns the K-th, the new threshold. Out of
+// line: it runs a few times per wave and row.
+__device__ __attribute__((noinline)) uint64_t wave_compact(uint64_t * buf, int * n, int K) {
     uint64_t v[kPerLane];
     const int lane = lane_id();
+    const int cnt = *n;
 #pragma unroll
     for (int j = 0; j < kPerLane; j++) {
         const int i = lane + kWave * j;
-        v[j] = i < n ? buf[i] : 0;
+        v[j] = i < cnt ? buf[i] : 0;
     }
     const uint64_t kth = wave_kth_largest(v, K);
     int pos = 0;
@@ -277,7 +279,7 @@ __device__ __forceinline__ uint64_t wave_compact(uint64_t * buf, int & n, int K)
         if (keep) buf[pos + lanes_below(m)] = v[j];
         pos += __popcll(m);
     }
-    n = pos;
+    *n = pos;
     return kth;
 }
 
@@ -289,77 +291,50 @@ struct WaveBuf {
     int K;
 };
 
-// Offers one entry per lane (valid lanes only) to the wave's buffer.
-__device__ __forceinline__ void wave_offer(WaveBuf & wb, bool valid, uint32_t key, uint32_t id) {
-    bool pass = valid && key >= wb.thr_key;
-    if (!ballot(pass)) return;
-    const uint64_t e = make_entry(key, id);
-    pass = pass && e > wb.thr;
-    uint64_t m = ballot(pass);
-    int cnt = __popcll(m);
-    if (wb.n + cnt > kCap) {
-        wb.thr = wave_compact(wb.buf, wb.n, wb.K);
-        wb.thr_key = entry_key(wb.thr);
-        pass = pass && e > wb.thr;
-        m = ballot(pass);
-        cnt = __popcll(m);
-    }
-    if (pass) wb.buf[wb.n + lanes_below(m)] = e;
-    wb.n += cnt;
-}
-
 // ------------------------------------------------------------------------------------------------------------------
-// Per-thread state of the streaming pass
+// Per-lane state of the streaming pass
 // ------------------------------------------------------------------------------------------------------------------
 
-struct TState {
-    uint64_t best;  // max make_entry(key(x), i): the first largest final logit (greedy)
-    uint64_t low;   // min make_entry(key(q), i) with the complement taken so the largest id wins ties: the last token
-    double s;       // sum of exp(q - m)
-    float m;        // running max of q
-    uint32_t flags;
+struct Lane {
+    float bestx;    // greedy: this lane's largest final logit, and the first id holding it
+    int besti;
+    float lowq;     // the smallest quotient and the largest id holding it: the last token of the order
+    int lowi;
+    float mx, mn;   // largest and smallest final logits (NaN ignored)
+    double s;       // sum of exp(q - m) ...
+    float m;        // ... against m, the wave's running largest quotient (the same in every lane)
+    uint32_t flags; // kNaN, kTempOver, kNaN0, kBadHist
 };
 
-__device__ inline void tstate_init(TState & st) {
-    st.best = 0;
-    st.low = ~0ull;
-    st.s = 0.0;
-    st.m = -FLT_MAX;
-    st.flags = 0;
-}
-
-// Flags of one final logit x under a flavor.
-__device__ inline uint32_t value_flags(float x) {
-    uint32_t f = 0;
-    if (__builtin_isnan(x)) f |= kNaN;
-    else if (x == INFINITY) f |= kPosInf;
-    else if (x == -INFINITY) f |= kNegInf;
-    else f |= kFinite;
-    return f;
+__device__ inline void lane_init(Lane & ln) {
+    ln.bestx = -INFINITY;
+    ln.besti = -1;
+    ln.lowq = INFINITY;
+    ln.lowi = -1;
+    ln.mx = -INFINITY;
+    ln.mn = INFINITY;
+    ln.s = 0.0;
+    ln.m = -FLT_MAX;
+    ln.flags = 0;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// Special tokens: history and banned ids of one chunk in LDS
+// Special tokens of one chunk in LDS: for each 32 tokens a pair of words, the history bits and the banned bits, and
+// the number of history tokens before them, so a history token finds its slot in O(1)
 // ------------------------------------------------------------------------------------------------------------------
 
 struct Specials {
-    uint32_t * bits;   // one bit per token of the chunk: history or banned
+    uint2 * bits;      // .x history, .y banned
+    int32_t * rank;    // history tokens before each word
     int32_t * slot_id; // history ids of the chunk, rising
     float * slot_raw;  // their raw logits, written by the stream
     int32_t * slot_cnt;
     int n_slots;
-    int min_banned, max_banned;  // banned ids of the chunk (INT_MAX / -1 when none)
     bool any;
 };
 
-__device__ inline int find_slot(const Specials & sp, int id) {
-    int lo = 0, hi = sp.n_slots;
-    while (lo < hi) {
-        const int mid = (lo + hi) >> 1;
-        if (sp.slot_id[mid] < id) lo = mid + 1;
-        else hi = mid;
-    }
-    return (lo < sp.n_slots && sp.slot_id[lo] == id) ? lo : -1;
+__device__ __forceinline__ int slot_of(const Specials & sp, int w, uint32_t hbits, int bit) {
+    return sp.rank[w] + __popc(hbits & ((1u << bit) - 1u));
 }
 
 template <int B>
@@ -367,12 +342,7 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
                                       const uint32_t * banned_row, int * red, uint32_t & bad) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
-    for (int w = tid; w < nw; w += B) sp.bits[w] = 0u;
-    int * shared_ints = red + 16;  // [0] min banned, [1] max banned
-    if (tid == 0) {
-        shared_ints[0] = 0x7fffffff;
-        shared_ints[1] = -1;
-    }
+    for (int w = tid; w < nw; w += B) sp.bits[w] = make_uint2(0u, 0u);
     __syncthreads();
     int h0 = 0, h1 = 0;
     if (pl.pen) {
@@ -384,19 +354,20 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
         }
         for (int j = h0 + tid; j < h1; j += B) {
             const int t = a.hist[j];
-            if (t >= c0 && t < c1) atomicOr(&sp.bits[(t - c0) >> 5], 1u << ((t - c0) & 31));
+            if (t >= c0 && t < c1) atomicOr(&sp.bits[(t - c0) >> 5].x, 1u << ((t - c0) & 31));
         }
     }
     __syncthreads();
-    // The slot list: history ids in rising order, each thread writing those of a run of words.
+    // Ranks and the slot list, each thread taking a run of words.
     const int wpt = (nw + B - 1) / B;
-    const int w0 = tid * wpt, w1 = min(nw, w0 + wpt);
+    const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
     int cnt = 0;
-    for (int w = w0; w < w1; w++) cnt += __popc(sp.bits[w]);
+    for (int w = w0; w < w1; w++) cnt += __popc(sp.bits[w].x);
     int total;
     int pos = block_excl_scan_i32<B>(cnt, red, total);
     for (int w = w0; w < w1; w++) {
-        uint32_t b = sp.bits[w];
+        sp.rank[w] = pos;
+        uint32_t b = sp.bits[w].x;
         while (b) {
             const int bit = __builtin_ctz(b);
             b &= b - 1;
@@ -411,8 +382,8 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
         for (int j = h0 + tid; j < h1; j += B) {
             const int t = a.hist[j];
             if (t >= c0 && t < c1) {
-                const int s = find_slot(sp, t);
-                atomicAdd(&sp.slot_cnt[s], 1);
+                const int o = t - c0;
+                atomicAdd(&sp.slot_cnt[slot_of(sp, o >> 5, sp.bits[o >> 5].x, o & 31)], 1);
             }
         }
     }
@@ -420,17 +391,10 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
         for (int w = tid; w < nw; w += B) {
             uint32_t bw = banned_row[(c0 >> 5) + w];
             const int base = c0 + (w << 5);
-            if (base + 32 > c1) bw &= (1u << (c1 - base)) - 1u;  // c1 - base < 32 here
-            if (bw) {
-                sp.bits[w] |= bw;
-                atomicMin(&shared_ints[0], base + __builtin_ctz(bw));
-                atomicMax(&shared_ints[1], base + 31 - __builtin_clz(bw));
-            }
+            if (base + 32 > c1) bw &= (1u << (c1 - base)) - 1u;  // 0 < c1 - base < 32 here
+            sp.bits[w].y = bw;
         }
     }
-    __syncthreads();
-    sp.min_banned = shared_ints[0];
-    sp.max_banned = shared_ints[1];
     __syncthreads();
 }
 
@@ -439,34 +403,38 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
 // ------------------------------------------------------------------------------------------------------------------
 
 struct RowTotals {
-    uint64_t best, low;
-    double s;   // sum of exp(q - m) ...
-    float m;    // ... relative to m
+    uint64_t best;  // greedy: make_entry(key, id) of the first largest final logit (0: none above -inf)
+    uint64_t low;   // (key << 32 | ~id) of the last token of the order (all ones: none)
+    double s;       // sum of exp(q - m) ...
+    float m;        // ... relative to m
+    float mx, mn;
     uint32_t flags;
 };
 
-// The row status from its flags, as the reference's checks order them; -1 when the row goes on.
-__device__ inline int row_status(const Plan & pl, const spx_row_params & p, uint32_t f, bool top_finite) {
+// The row status, as the reference's checks order them; -1 when the row goes on.
+__device__ inline int row_status(const Plan & pl, const spx_row_params & p, const RowTotals & t, bool top_finite) {
+    const uint32_t f = t.flags;
     if (pl.mode == kInvalid || (f & kBadHist)) return SPX_ROW_INVALID_PARAMS;
     const bool pen = !neutral(p);
+    const bool posinf = t.mx == INFINITY;
     if (pl.flavor == SPX_FLAVOR_TRANSFORMERS) {
-        // restricted(): std::max_element's largest, NaN in front of all (src/families/qwen3-tts/sampler.cpp:43-49)
+        // restricted(): std::max_element's largest, a NaN in front taken as it (src/families/qwen3-tts/sampler.cpp:43-49)
         if (f & kNaN0) return SPX_ROW_NO_FINITE_LOGIT;
-        if (f & kPosInf) return pen ? SPX_ROW_REP_PENALTY_OVERFLOW : SPX_ROW_NO_FINITE_LOGIT;
-        if (!(f & kFinite)) return SPX_ROW_NO_FINITE_LOGIT;
+        if (posinf) return pen ? SPX_ROW_REP_PENALTY_OVERFLOW : SPX_ROW_NO_FINITE_LOGIT;
+        if (!(t.mx > -INFINITY)) return SPX_ROW_NO_FINITE_LOGIT;
         if (pl.mode == kGreedy) return -1;
         if (f & kNaN) return SPX_ROW_NONFINITE_INPUT;
         if (!top_finite) return SPX_ROW_TEMPERATURE_OVERFLOW;  // qwen3-tts/sampler.cpp:82-83
         return -1;
     }
-    if (!(f & kNaN0) && (f & kPosInf) && pen) return SPX_ROW_REP_PENALTY_OVERFLOW;
+    if (!(f & kNaN0) && posinf && pen) return SPX_ROW_REP_PENALTY_OVERFLOW;
     if (pl.flavor == SPX_FLAVOR_HARU) {
-        if (f & (kNaN | kPosInf)) return SPX_ROW_NONFINITE_INPUT;  // haru/sampler.cpp:21-23
+        if ((f & kNaN) || posinf) return SPX_ROW_NONFINITE_INPUT;  // haru/sampler.cpp:21-23
         if (pl.mode == kGreedy) return -1;
         if (f & kTempOver) return SPX_ROW_TEMPERATURE_OVERFLOW;  // haru/sampler.cpp:33-35
         return -1;
     }
-    if (f & (kNaN | kPosInf | kNegInf)) return SPX_ROW_NONFINITE_INPUT;  // drama3/sampler.cpp:35-37
+    if ((f & kNaN) || posinf || t.mn == -INFINITY) return SPX_ROW_NONFINITE_INPUT;  // drama3/sampler.cpp:35-37
     if (pl.mode == kGreedy) return -1;
     if (!top_finite) return SPX_ROW_TEMPERATURE_OVERFLOW;  // drama3/sampler.cpp:46-47
     return -1;
@@ -494,14 +462,14 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
     const int tid = threadIdx.x;
     const double u = a.u ? a.u[row] : 0.0;
     const float top = n > 0 ? entry_value(e[0]) : -INFINITY;
-    const int st = row_status(pl, p, tot.flags, n > 0 && __builtin_isfinite(top));
+    const int st = row_status(pl, p, tot, n > 0 && __builtin_isfinite(top));
     if (st >= 0) {
         if (tid == 0) write_row(a, row, -1, st, 0);
         return true;
     }
     if (pl.mode == kGreedy) {
         // std::max_element: the first largest, or token 0 when its logit is NaN.
-        const int id = (tot.flags & kNaN0) ? 0 : (int) entry_id(tot.best);
+        const int id = ((tot.flags & kNaN0) || tot.best == 0) ? 0 : (int) entry_id(tot.best);
         if (tid == 0) {
             write_row(a, row, id, SPX_ROW_OK, 1);
             if (a.out_cand_ids) {
@@ -684,199 +652,278 @@ __device__ inline float load_one<uint16_t>(const uint16_t * p) {
     return bf16_to_float(*p);
 }
 
+using U32x4 = uint32_t __attribute__((ext_vector_type(4)));
+
 template <typename T>
 struct Vec;
 template <>
 struct Vec<float> {
     static constexpr int n = 4;
-    using raw = float4;
-    __device__ static inline void unpack(const raw & r, float (&x)[4]) {
-        x[0] = r.x;
-        x[1] = r.y;
-        x[2] = r.z;
-        x[3] = r.w;
+    __device__ static inline void unpack(const U32x4 & r, float (&x)[4]) {
+        x[0] = __uint_as_float(r.x);
+        x[1] = __uint_as_float(r.y);
+        x[2] = __uint_as_float(r.z);
+        x[3] = __uint_as_float(r.w);
     }
 };
 template <>
 struct Vec<uint16_t> {
     static constexpr int n = 8;
-    using raw = uint4;
-    __device__ static inline void unpack(const raw & r, float (&x)[8]) {
-        const uint32_t w[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            x[2 * i] = __uint_as_float(w[i] << 16);
-            x[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
-        }
+    __device__ static inline void unpack(const U32x4 & r, float (&x)[8]) {
+        x[0] = __uint_as_float(r.x << 16);
+        x[1] = __uint_as_float(r.x & 0xffff0000u);
+        x[2] = __uint_as_float(r.y << 16);
+        x[3] = __uint_as_float(r.y & 0xffff0000u);
+        x[4] = __uint_as_float(r.z << 16);
+        x[5] = __uint_as_float(r.z & 0xffff0000u);
+        x[6] = __uint_as_float(r.w << 16);
+        x[7] = __uint_as_float(r.w & 0xffff0000u);
     }
 };
 
-// One final logit x of token i: the statistics and the candidate offer of its row's mode. `live` is false for
-// lanes past the chunk's end and for special tokens the post-pass handles instead.
-__device__ __forceinline__ void take(const Plan & pl, TState & st, WaveBuf & wb, bool live, float x, int i) {
+// The wave's candidate offers of one vector: lanes of `ok` whose quotient reaches tf enter the buffer, after a
+// compaction where the buffer would overflow (which raises tf to the wave's new K-th key).
+template <int V>
+__device__ __forceinline__ void offer_vec(WaveBuf & wb, uint32_t * wg_tau, const float (&q)[V], uint32_t ok, float & tf,
+                                          int i0) {
+    uint64_t m[V];
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+        m[j] = ballot(((ok >> j) & 1u) && q[j] >= tf);
+        cnt += (int) __popcll(m[j]);
+    }
+    if (cnt == 0) return;
+    if (wb.n + cnt > kCap) {
+        wb.thr = wave_compact(wb.buf, &wb.n, wb.K);
+        wb.thr_key = entry_key(wb.thr);
+        tf = key_float(wb.thr_key);
+        if (lane_id() == 0) atomicMax(wg_tau, wb.thr_key);
+#pragma unroll
+        for (int j = 0; j < V; j++) m[j] = ballot(((ok >> j) & 1u) && q[j] >= tf);
+    }
+#pragma unroll
+    for (int j = 0; j < V; j++) {
+        if (m[j]) {
+            if (((ok >> j) & 1u) && q[j] >= tf)
+                wb.buf[wb.n + lanes_below(m[j])] = make_entry(order_key(q[j]), (uint32_t) (i0 + j));
+            wb.n += (int) __popcll(m[j]);
+        }
+    }
+}
+
+// U vectors of V final logits per lane; vector u holds tokens i0[u] .. i0[u]+V-1. Bit j of live[u] is set where token
+// i0[u]+j is this lane's to take, and of ban[u] where that token is banned (its x is -inf). x of a token not live is
+// -inf or a copy of one taken elsewhere, so the group's largest x is a largest final logit. Every lane takes part.
+template <int U, int V>
+__device__ __forceinline__ void take_group(const Plan & pl, Lane & ln, WaveBuf & wb, uint32_t * wg_tau,
+                                           const float (&x)[U][V], const uint32_t (&live)[U], const uint32_t (&ban)[U],
+                                           const int (&i0)[U]) {
+    float gx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+#pragma unroll
+        for (int j = 0; j < V; j++) gx = fmaxf(gx, x[u][j]);
+    }
+    ln.mx = fmaxf(ln.mx, gx);
+    if (pl.flavor == SPX_FLAVOR_FISH) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int j = 0; j < V; j++) ln.mn = fminf(ln.mn, ((live[u] >> j) & 1u) ? x[u][j] : INFINITY);
+        }
+    }
     if (pl.mode == kGreedy) {
-        if (live) {
-            st.flags |= value_flags(x);
-            if (i == 0 && __builtin_isnan(x)) st.flags |= kNaN0;
-            if (!__builtin_isnan(x)) {
-                const uint64_t e = make_entry(order_key(x), (uint32_t) i);
-                st.best = e > st.best ? e : st.best;
+        // tokens come to a lane by rising id: the first largest is the first strictly above all before it
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+#pragma unroll
+            for (int j = 0; j < V; j++) {
+                if (((live[u] >> j) & 1u) && x[u][j] > ln.bestx) {
+                    ln.bestx = x[u][j];
+                    ln.besti = i0[u] + j;
+                }
+                if (((live[u] >> j) & 1u) && __builtin_isnan(x[u][j])) ln.flags |= kNaN;
             }
         }
         return;
     }
-    float q = -INFINITY;
-    uint32_t key = 0;
-    if (live) {
-        const uint32_t f = value_flags(x);
-        st.flags |= f;
-        if (i == 0 && __builtin_isnan(x)) st.flags |= kNaN0;
-        q = div_rn(x, pl.t, pl.rt);
-        if ((f & kFinite) && !__builtin_isfinite(q)) st.flags |= kTempOver;
-        if (!__builtin_isnan(q)) {
-            key = order_key(q);
-            if (pl.need_low) {
-                const uint64_t e = ((uint64_t) key << 32) | (uint64_t) (~(uint32_t) i);
-                st.low = e < st.low ? e : st.low;
-            }
-        } else {
-            q = -INFINITY;
-        }
-    }
     if (pl.need_s) {
-        if (q > st.m) {
-            st.s *= exp((double) st.m - (double) q);
-            st.m = q;
+        // The wave's reference for the sum of exp: its largest quotient so far. Division by t > 0 rounded to nearest
+        // keeps the order, so the group's largest quotient is its largest logit divided.
+        const float wx = wave_max_f32(gx);
+        if (wx > -INFINITY) {
+            const float wm = div_rn(wx, pl.t, pl.rt);
+            if (wm > ln.m) {
+                ln.s *= exp((double) ln.m - (double) wm);
+                ln.m = wm;
+            }
         }
-        st.s += (double) __builtin_amdgcn_exp2f((q - st.m) * 1.4426950408889634f);
     }
-    wave_offer(wb, live && key != 0, key, (uint32_t) i);
+    const uint32_t tk = max(wb.thr_key, *(volatile uint32_t *) wg_tau);
+    float tf = tk ? key_float(tk) : -INFINITY;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        const uint32_t act = live[u] & ~ban[u];  // tokens whose quotient is computed
+        float q[V];
+        uint32_t nan = 0;
+#pragma unroll
+        for (int j = 0; j < V; j++) {
+            // x / t by Markstein's correction, the IEEE division where the quotient leaves the normal range
+            const float xv = x[u][j];
+            const float q0 = xv * pl.rt;
+            float qq = __builtin_fmaf(__builtin_fmaf(-q0, pl.t, xv), pl.rt, q0);
+            const float aq = __builtin_fabsf(q0);
+            if (__builtin_expect(((act >> j) & 1u) && !(aq >= 0x1p-125f && aq < INFINITY), 0)) qq = xv / pl.t;
+            if (pl.flavor == SPX_FLAVOR_HARU && ((act >> j) & 1u) && __builtin_isfinite(xv) && !__builtin_isfinite(qq))
+                ln.flags |= kTempOver;
+            qq = ((act >> j) & 1u) ? qq : -INFINITY;
+            nan |= __builtin_isnan(qq) ? (1u << j) : 0u;
+            q[j] = qq;
+        }
+        if (nan) ln.flags |= kNaN;
+        const uint32_t ok = act & ~nan;
+        if (pl.need_low) {
+#pragma unroll
+            for (int j = 0; j < V; j++) {
+                // banned tokens are the last of the order, -inf
+                const float qv = ((ban[u] >> j) & 1u) ? -INFINITY : q[j];
+                if ((((ok | ban[u]) & live[u]) >> j & 1u) && qv <= ln.lowq) {
+                    ln.lowq = qv;
+                    ln.lowi = i0[u] + j;
+                }
+            }
+        }
+        if (pl.need_s) {
+#pragma unroll
+            for (int j = 0; j < V; j++) ln.s += (double) __builtin_amdgcn_exp2f((q[j] - ln.m) * 1.4426950408889634f);
+        }
+        offer_vec<V>(wb, wg_tau, q, ok, tf, i0[u]);
+    }
+}
+
+// The special tokens among V consecutive tokens at chunk offset `off`: a history token is set aside for the post-pass
+// (its raw logit to its slot, -inf in x, out of `live`), a banned one becomes -inf and is marked in `ban`.
+template <int V>
+__device__ __forceinline__ void special_vec(const Specials & sp, float (&x)[V], uint32_t & live, uint32_t & ban, int off,
+                                            bool in) {
+    const uint2 pair = in ? sp.bits[off >> 5] : make_uint2(0u, 0u);
+    const int sh = off & 31;
+    const uint32_t mask = (1u << V) - 1u;
+    const uint32_t nh = (pair.x >> sh) & mask, nb = (pair.y >> sh) & mask & ~nh;
+    if (ballot(nh != 0)) {
+        if (nh) {
+            const int base = sp.rank[off >> 5];
+#pragma unroll
+            for (int j = 0; j < V; j++) {
+                if ((nh >> j) & 1u) sp.slot_raw[base + __popc(pair.x & ((1u << (sh + j)) - 1u))] = x[j];
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < V; j++) x[j] = ((nh >> j) & 1u) ? -INFINITY : x[j];
+        live &= ~nh;
+    }
+    if (ballot(nb != 0)) {
+#pragma unroll
+        for (int j = 0; j < V; j++) x[j] = ((nb >> j) & 1u) ? -INFINITY : x[j];
+        ban = nb;
+    }
 }
 
 template <typename T, int B>
 __device__ __forceinline__ void stream_chunk(const Launch & a, const T * rowp, int c0, int c1, const Plan & pl,
-                                    const Specials & sp, TState & st, WaveBuf & wb) {
+                                             const Specials & sp, Lane & ln, WaveBuf & wb, uint32_t * wg_tau) {
     constexpr int V = Vec<T>::n;
     const int n = c1 - c0;
     const int tid = threadIdx.x;
+    int done = 0;
     if (a.vec_ok) {
-        const int ng = n / V;  // whole vectors; the tail below
-        const typename Vec<T>::raw * vp = (const typename Vec<T>::raw *) (rowp + c0);
-        using Raw = typename Vec<T>::raw;
-        // One vector of V tokens per lane: special tokens set aside for the post-pass, the rest taken.
-        auto process = [&](const Raw & rv, int g) __attribute__((always_inline)) {
-            const bool in = g < ng;
-            float x[V];
-            Vec<T>::unpack(rv, x);
-            uint32_t nib = 0;
-            if (sp.any && in) {
-                const int off = g * V;
-                nib = (sp.bits[off >> 5] >> (off & 31)) & ((1u << V) - 1u);
-            }
-            if (ballot(nib != 0)) {
-                if (nib) {
-#pragma unroll
-                    for (int j = 0; j < V; j++) {
-                        if (nib & (1u << j)) {
-                            const int s = find_slot(sp, c0 + g * V + j);
-                            if (s >= 0) sp.slot_raw[s] = x[j];
-                        }
-                    }
-                }
-            }
-#pragma unroll
-            for (int j = 0; j < V; j++) take(pl, st, wb, in && !((nib >> j) & 1u), in ? x[j] : 0.0f, c0 + g * V + j);
-        };
-        const Raw zero = {};
-        // Four vectors in flight per lane before any is processed.
+        const int ng = n / V;  // whole vectors
+        const U32x4 * vp = (const U32x4 *) (rowp + c0);
+        // Four 16-byte loads in flight per lane before any is used; lanes past the end load the last vector again
+        // and take nothing from it.
         for (int base = 0; base < ng; base += 4 * B) {
             const int g0 = base + tid, g1 = g0 + B, g2 = g1 + B, g3 = g2 + B;
-            const Raw r0 = g0 < ng ? vp[g0] : zero;
-            const Raw r1 = g1 < ng ? vp[g1] : zero;
-            const Raw r2 = g2 < ng ? vp[g2] : zero;
-            const Raw r3 = g3 < ng ? vp[g3] : zero;
-            process(r0, g0);
-            process(r1, g1);
-            process(r2, g2);
-            process(r3, g3);
-        }
-        // The tail: fewer than V elements.
-        const int t0 = ng * V;
-        if (t0 < n) {
-            const int i = t0 + tid;
-            const bool in = tid < V && i < n;
-            float x = in ? load_one<T>(rowp + c0 + i) : 0.0f;
-            bool live = in;
-            if (in && sp.any && ((sp.bits[i >> 5] >> (i & 31)) & 1u)) {
-                const int s = find_slot(sp, c0 + i);
-                if (s >= 0) sp.slot_raw[s] = x;
-                live = false;
+            const U32x4 r0 = vp[min(g0, ng - 1)];
+            const U32x4 r1 = vp[min(g1, ng - 1)];
+            const U32x4 r2 = vp[min(g2, ng - 1)];
+            const U32x4 r3 = vp[min(g3, ng - 1)];
+            float x[4][V];
+            Vec<T>::unpack(r0, x[0]);
+            Vec<T>::unpack(r1, x[1]);
+            Vec<T>::unpack(r2, x[2]);
+            Vec<T>::unpack(r3, x[3]);
+            const int g[4] = {g0, g1, g2, g3};
+            uint32_t live[4], ban[4];
+            int i0[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const bool in = g[u] < ng;
+                live[u] = in ? (1u << V) - 1u : 0u;
+                ban[u] = 0u;
+                i0[u] = c0 + g[u] * V;
+                if (sp.any) special_vec<V>(sp, x[u], live[u], ban[u], g[u] * V, in);
             }
-            // Every lane of a wave takes part in the offer.
-            take(pl, st, wb, live, x, c0 + i);
+            take_group<4, V>(pl, ln, wb, wg_tau, x, live, ban, i0);
         }
-    } else {
-        for (int base = 0; base < n; base += B) {
-            const int i = base + tid;
-            const bool in = i < n;
-            float x = in ? load_one<T>(rowp + c0 + i) : 0.0f;
-            bool live = in;
-            if (in && sp.any && ((sp.bits[i >> 5] >> (i & 31)) & 1u)) {
-                const int s = find_slot(sp, c0 + i);
-                if (s >= 0) sp.slot_raw[s] = x;
-                live = false;
-            }
-            take(pl, st, wb, live, x, c0 + i);
-        }
+        done = ng * V;
+    }
+    // One token per lane: a row that is not 16-byte aligned, and the tail of one that is.
+    for (int base = done; base < n; base += B) {
+        const int i = base + tid;
+        const bool in = i < n;
+        float x[1][1] = {{in ? load_one<T>(rowp + c0 + i) : -INFINITY}};
+        uint32_t live[1] = {in ? 1u : 0u}, ban[1] = {0u};
+        const int i0[1] = {c0 + i};
+        if (sp.any) special_vec<1>(sp, x[0], live[0], ban[0], i, in);
+        take_group<1, 1>(pl, ln, wb, wg_tau, x, live, ban, i0);
     }
 }
 
-// The history tokens of the chunk, after the stream: penalties, then the ban, then the same statistics.
+// The history tokens of the chunk, after the stream: penalties, the ban, then the same statistics.
 template <int B>
-__device__ __forceinline__ void take_specials(const Launch & a, const spx_row_params & p, const Plan & pl, const Specials & sp,
-                                     const uint32_t * banned_row, TState & st, WaveBuf & wb) {
+__device__ __forceinline__ void take_specials(const spx_row_params & p, const Plan & pl, const Specials & sp,
+                                              const uint32_t * banned_row, Lane & ln, WaveBuf & wb, uint32_t * wg_tau) {
     for (int base = 0; base < sp.n_slots; base += B) {
         const int s = base + threadIdx.x;
         const bool in = s < sp.n_slots;
-        float x = 0.0f;
-        int id = 0;
+        float x[1][1] = {{-INFINITY}};
+        int i0[1] = {0};
+        uint32_t live[1] = {in ? 1u : 0u}, ban[1] = {0u};
         if (in) {
-            id = sp.slot_id[s];
-            x = penalize(sp.slot_raw[s], pl.counts ? sp.slot_cnt[s] : 0, p);
-            if (banned_row && ((banned_row[id >> 5] >> (id & 31)) & 1u)) x = -INFINITY;
+            const int id = sp.slot_id[s];
+            float v = penalize(sp.slot_raw[s], pl.counts ? sp.slot_cnt[s] : 0, p);
+            if (banned_row && ((banned_row[id >> 5] >> (id & 31)) & 1u)) {
+                v = -INFINITY;
+                ban[0] = 1u;
+            }
+            if (id == 0 && __builtin_isnan(v)) ln.flags |= kNaN0;
+            x[0][0] = v;
+            i0[0] = id;
         }
-        take(pl, st, wb, in, x, id);
-    }
-    // Banned tokens outside the history: -inf. They matter for the first largest of an all -inf row and for the
-    // last token of an order, where they come last.
-    if (threadIdx.x == 0 && sp.min_banned <= sp.max_banned) {
-        st.flags |= kNegInf;
-        const uint64_t e = make_entry(order_key(-INFINITY), (uint32_t) sp.min_banned);
-        if (pl.mode == kGreedy) st.best = e > st.best ? e : st.best;
-        if (pl.need_low) {
-            const uint64_t l = ((uint64_t) order_key(-INFINITY) << 32) | (uint64_t) (~(uint32_t) sp.max_banned);
-            st.low = l < st.low ? l : st.low;
-        }
+        take_group<1, 1>(pl, ln, wb, wg_tau, x, live, ban, i0);
     }
 }
 
-// Reduces the threads' states to thread 0's, through LDS.
+// Reduces the lanes' states over the work-group, through LDS; every thread gets the totals.
 template <int B>
-__device__ inline RowTotals reduce_states(TState st, uint64_t * red64, double * redd, float * redf, uint32_t * redu) {
+__device__ inline RowTotals reduce_lanes(const Lane & ln, uint64_t * red64, double * redd, float * redf, uint32_t * redu) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
-    // m first, so the sums can be brought to one reference
-    float m = st.m;
-    for (int o = 32; o >= 1; o >>= 1) m = fmaxf(m, __shfl_xor(m, o, kWave));
-    double s = st.s * ((st.m == m) ? 1.0 : exp((double) st.m - (double) m));
-    s = wave_sum_f64(s);
-    const uint64_t best = wave_max_u64(st.best);
-    const uint64_t low = wave_min_u64(st.low);
-    const uint32_t flags = wave_or_u32(st.flags);
+    const uint64_t be = ln.besti >= 0 ? make_entry(order_key(ln.bestx), (uint32_t) ln.besti) : 0;
+    const uint64_t lo = ln.lowi >= 0 ? (((uint64_t) order_key(ln.lowq) << 32) | (uint64_t) (~(uint32_t) ln.lowi)) : ~0ull;
+    const uint64_t best = wave_max_u64(be);
+    const uint64_t low = wave_min_u64(lo);
+    const double s = wave_sum_f64(ln.s);  // m is the same in every lane of a wave
+    const float mx = wave_max_f32(ln.mx);
+    const float mn = -wave_max_f32(-ln.mn);
+    const uint32_t flags = wave_or_u32(ln.flags);
     if (lane == 0) {
         red64[2 * wave] = best;
         red64[2 * wave + 1] = low;
         redd[wave] = s;
-        redf[wave] = m;
+        redf[4 * wave] = ln.m;
+        redf[4 * wave + 1] = mx;
+        redf[4 * wave + 2] = mn;
         redu[wave] = flags;
     }
     __syncthreads();
@@ -884,14 +931,18 @@ __device__ inline RowTotals reduce_states(TState st, uint64_t * red64, double * 
     t.best = 0;
     t.low = ~0ull;
     t.m = -FLT_MAX;
+    t.mx = -INFINITY;
+    t.mn = INFINITY;
     t.flags = 0;
     t.s = 0;
-    for (int w = 0; w < B / kWave; w++) t.m = fmaxf(t.m, redf[w]);
+    for (int w = 0; w < B / kWave; w++) t.m = fmaxf(t.m, redf[4 * w]);
     for (int w = 0; w < B / kWave; w++) {
         t.best = red64[2 * w] > t.best ? red64[2 * w] : t.best;
         t.low = red64[2 * w + 1] < t.low ? red64[2 * w + 1] : t.low;
         t.flags |= redu[w];
-        t.s += redd[w] * ((redf[w] == t.m) ? 1.0 : exp((double) redf[w] - (double) t.m));
+        t.mx = fmaxf(t.mx, redf[4 * w + 1]);
+        t.mn = fminf(t.mn, redf[4 * w + 2]);
+        t.s += redd[w] * ((redf[4 * w] == t.m) ? 1.0 : exp((double) redf[4 * w] - (double) t.m));
     }
     __syncthreads();
     return t;
@@ -905,12 +956,10 @@ __device__ inline int union_and_sort(uint64_t * wave_bufs, const int * wave_n, c
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     uint64_t floor = 0;
     for (int w = 0; w < B / kWave; w++) floor = wave_thr[w] > floor ? wave_thr[w] : floor;
-    // counts per wave
     const int n = wave_n[wave];
     const uint64_t * src = wave_bufs + wave * kCap;
     int mine = 0;
-    for (int i = lane; i < n; i += kWave) mine += src[i] >= floor ? 1 : 0;
-    mine = wave_sum_i32(mine);
+    for (int i0 = 0; i0 < n; i0 += kWave) mine += (int) __popcll(ballot(i0 + lane < n && src[i0 + lane] >= floor));
     if (lane == 0) red[wave] = mine;
     __syncthreads();
     int base = 0, total = 0;
@@ -926,7 +975,7 @@ __device__ inline int union_and_sort(uint64_t * wave_bufs, const int * wave_n, c
         const bool keep = i < n && src[i] >= floor;
         const uint64_t m = ballot(keep);
         if (keep && pos + lanes_below(m) < cap) dst[pos + lanes_below(m)] = src[i];
-        pos += __popcll(m);
+        pos += (int) __popcll(m);
     }
     int np2 = 1;
     while (np2 < total) np2 <<= 1;
@@ -947,205 +996,16 @@ __device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & sp
 }
 
 
-// Lists a row for the multi-pass path with what that path needs of it.
-__device__ inline void defer_row(const Launch & a, int row, const RowTotals & t, const uint64_t * sorted, int n) {
-    const int slot = atomicAdd(&a.fb_count[0], 1);
-    a.fb_rows[slot] = row;
-    RowState & rs = a.row_state[row];
-    rs.m = t.m;
-    rs.s = t.s;
-    rs.low = t.low;
-    rs.flags = t.flags;
-    rs.top = n > 0 ? entry_value(sorted[0]) : -INFINITY;
-}
-
-template <typename T>
-__global__ __launch_bounds__(kBlock) void stream_kernel(Launch a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int B = kBlock;
-    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
-    int row, split;
-    xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
-    if (row >= a.rows) return;
-
-    spx_row_params p;
-    if (a.params) {
-        p = a.params[row];
-    } else {
-        // spx_argmax_rows: std::max_element of the suppressed logits
-        p.flavor = SPX_FLAVOR_TRANSFORMERS;
-        p.greedy = 1;
-        p.temperature = 1.0f;
-        p.top_k = 0;
-        p.top_p = 1.0f;
-        p.repetition_penalty = 1.0f;
-        p.presence_penalty = 0.0f;
-        p.frequency_penalty = 0.0f;
-    }
-    const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr);
-    const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
-    const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
-
-    int * ired = (int *) (lds + a.off_red);
-    double * dred = (double *) (lds + a.off_red + 256);
-    uint64_t * red64 = (uint64_t *) (lds + a.off_red + 512);
-    float * fred = (float *) (lds + a.off_red + 768);
-    uint32_t * ured = (uint32_t *) (lds + a.off_red + 832);
-    int * wave_n = (int *) (lds + a.off_red + 896);
-    uint64_t * wave_thr = (uint64_t *) (lds + a.off_red + 960);
-
-    TState st;
-    tstate_init(st);
-    Specials sp;
-    sp.any = false;
-    sp.n_slots = 0;
-    sp.min_banned = 0x7fffffff;
-    sp.max_banned = -1;
-    sp.bits = (uint32_t *) (lds + a.off_bits);
-    sp.slot_id = (int32_t *) (lds + a.off_slots);
-    sp.slot_raw = (float *) (lds + a.off_slots + 4 * a.slot_cap);
-    sp.slot_cnt = (int32_t *) (lds + a.off_slots + 8 * a.slot_cap);
-    uint32_t bad = 0;
-    if (pl.mode != kInvalid && (pl.pen || banned_row)) {
-        sp.any = true;
-        build_specials<B>(sp, a, row, c0, c1, pl, banned_row, ired, bad);
-    }
-    st.flags |= bad;
-
-    const bool sampling = pl.mode == kTopK || pl.mode == kFull;
-    WaveBuf wb;
-    wb.buf = (uint64_t *) (lds + a.off_cand) + wave * kCap;
-    wb.n = 0;
-    wb.thr = (uint64_t) 1 << 32;
-    wb.thr_key = 1;
-    wb.K = pl.kc;
-
-    if (pl.mode != kInvalid) {
-        const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
-        stream_chunk<T, B>(a, rowp, c0, c1, pl, sp, st, wb);
-        if (sp.any) {
-            __syncthreads();
-            take_specials<B>(a, p, pl, sp, banned_row, st, wb);
-        }
-    }
-
-    // Each wave keeps exactly its top K; its K-th entry bounds the row's K-th from below.
-    uint64_t thr = 0;
-    if (sampling) {
-        if (wb.n > wb.K) {
-            thr = wave_compact(wb.buf, wb.n, wb.K);
-        } else if (wb.n == wb.K) {
-            uint64_t m = ~0ull;
-            for (int i = lane; i < wb.n; i += kWave) m = wb.buf[i] < m ? wb.buf[i] : m;
-            thr = wave_min_u64(m);
-        }
-    }
-    if (lane == 0) {
-        wave_n[wave] = sampling ? wb.n : 0;
-        wave_thr[wave] = thr;
-    }
-    const RowTotals tot = reduce_states<B>(st, red64, dred, fred, ured);  // its barriers publish wave_n
-
-    uint64_t * sorted = (uint64_t *) (lds + a.off_sort);
-    int n = 0;
-    bool complete = true;
-    if (sampling) {
-        n = union_and_sort<B>((uint64_t *) (lds + a.off_cand), wave_n, wave_thr, sorted, a.sort_cap, ired);
-        complete = n < pl.kc;  // fewer than K: no wave ever dropped an entry
-        n = min(n, pl.kc);
-    }
-
-    FinishLds L;
-    L.w = (double *) (lds + a.off_cand);
-    L.red = dred;
-    L.ired = ired;
-    L.pf = (float *) (lds + a.off_cand + 8 * kKeep);
-
-    if (a.splits > 1) {
-        // Publish this chunk's partial; the last chunk of the row to arrive merges them.
-        Partial * part = a.partials + (int64_t) row * a.splits + split;
-        uint64_t * pc = a.part_cands + ((int64_t) row * a.splits + split) * kKeep;
-        for (int i = tid; i < n; i += B) pc[i] = sorted[i];
-        if (tid == 0) {
-            part->best = tot.best;
-            part->low = tot.low;
-            part->s = tot.s;
-            part->m = tot.m;
-            part->flags = tot.flags;
-            part->n = n;
-            part->complete = complete ? 1 : 0;
-            part->kth = (n >= pl.kc && n > 0) ? sorted[n - 1] : 0;
-        }
-        __threadfence();
-        __syncthreads();
-        if (tid == 0) {
-            const unsigned prev = atomicAdd(&a.counters[row], 1u);
-            ired[0] = prev == (unsigned) (a.splits - 1);
-        }
-        __syncthreads();
-        if (!ired[0]) return;
-        __threadfence();
-        if (tid == 0) a.counters[row] = 0;  // ready for the next launch
-        RowTotals t;
-        t.best = 0;
-        t.low = ~0ull;
-        t.flags = 0;
-        t.m = -FLT_MAX;
-        t.s = 0;
-        uint64_t floor = 0;
-        bool all_complete = true;
-        const Partial * pr = a.partials + (int64_t) row * a.splits;
-        for (int s2 = 0; s2 < a.splits; s2++) {
-            const Partial q = pr[s2];
-            t.best = q.best > t.best ? q.best : t.best;
-            t.low = q.low < t.low ? q.low : t.low;
-            t.flags |= q.flags;
-            t.m = fmaxf(t.m, q.m);
-            floor = q.kth > floor ? q.kth : floor;
-            all_complete = all_complete && q.complete;
-        }
-        for (int s2 = 0; s2 < a.splits; s2++) {
-            const Partial q = pr[s2];
-            t.s += q.s * ((q.m == t.m) ? 1.0 : exp((double) q.m - (double) t.m));
-        }
-        int total = 0;
-        if (sampling) {
-            for (int s2 = 0; s2 < a.splits; s2++) {
-                const int ns = pr[s2].n;
-                const uint64_t * src = a.part_cands + ((int64_t) row * a.splits + s2) * kKeep;
-                for (int i0 = 0; i0 < ns; i0 += B) {
-                    const int i = i0 + tid;
-                    const bool keep = i < ns && src[i] >= floor;
-                    int cnt_total;
-                    const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, ired + 32, cnt_total);
-                    if (keep && total + pos < a.sort_cap) sorted[total + pos] = src[i];
-                    total += cnt_total;
-                }
-            }
-            total = min(total, a.sort_cap);
-            int np2 = 1;
-            while (np2 < total) np2 <<= 1;
-            for (int i = total + tid; i < np2; i += B) sorted[i] = 0;
-            __syncthreads();
-            block_sort_desc<B>(sorted, np2);
-        }
-        n = min(total, pl.kc);
-        if (!finish_row<B>(a, row, p, pl, t, sorted, n, all_complete, L)) {
-            if (tid == 0) defer_row(a, row, t, sorted, n);
-        }
-        return;
-    }
-    if (!finish_row<B>(a, row, p, pl, tot, sorted, n, complete, L)) {
-        if (tid == 0) defer_row(a, row, tot, sorted, n);
-    }
-}
-
 // ------------------------------------------------------------------------------------------------------------------
 // The multi-pass path: exact radix selects over the whole row
 // ------------------------------------------------------------------------------------------------------------------
 
 // Fixed-point scale of the masses the selects add up: exact, order-free sums of exp(q - top) rounded to 2^-40.
 constexpr double kFix = 1099511627776.0;  // 2^40
+
+__device__ __forceinline__ uint64_t mass_fixed(float q, float top) {
+    return (uint64_t) (exp((double) q - (double) top) * kFix + 0.5);
+}
 
 struct Select {
     uint64_t prefix;   // the high `bits` bits of the entry fixed so far
@@ -1156,7 +1016,7 @@ struct Select {
     uint64_t own_m;    // its own mass
 };
 
-// One row's whole-vocabulary state in the fallback work-group.
+// One row's whole-vocabulary state in the work-group that resolves it.
 struct FbRow {
     const Launch * a;
     int row;
@@ -1164,37 +1024,62 @@ struct FbRow {
     Plan pl;
     Specials sp;
     const uint32_t * banned_row;
-    float top;       // the largest final quotient
-    float * spec_q;  // the final quotient of each history slot
+    float top;  // the largest final quotient
+    int * ired;
 };
 
-// Visits every token's entry and fixed-point mass; banned tokens and NaN quotients carry neither.
+// Visits every token's entry and fixed-point mass (a NaN quotient carries neither), chunk by chunk, each chunk's
+// special tokens rebuilt in LDS as the stream had them: a banned token as -inf, a history token by its final quotient.
 template <typename T, int B, typename F>
-__device__ inline void fb_visit(const FbRow & r, F && f) {
+__device__ inline void fb_visit(FbRow & r, F && f) {
     const Launch & a = *r.a;
     const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
-    const int n = a.vocab;
-    for (int i = threadIdx.x; i < n; i += B) {
-        if (r.sp.any && ((r.sp.bits[i >> 5] >> (i & 31)) & 1u)) continue;
-        const float x = load_one<T>(rowp + i);
-        const float q = div_rn(x, r.pl.t, r.pl.rt);
-        if (__builtin_isnan(q)) continue;
-        const double w = exp((double) q - (double) r.top);
-        f(make_entry(order_key(q), (uint32_t) i), (uint64_t) (w * kFix + 0.5));
+    const bool spec = r.pl.pen || r.banned_row;
+    for (int c0 = 0; c0 < a.vocab; c0 += a.chunk) {
+        const int c1 = min(a.vocab, c0 + a.chunk);
+        if (spec) {
+            __syncthreads();  // the previous chunk's special tokens are read no more
+            uint32_t bad = 0;
+            build_specials<B>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.ired, bad);
+            for (int s = threadIdx.x; s < r.sp.n_slots; s += B) {
+                const int id = r.sp.slot_id[s];
+                float v = penalize(load_one<T>(rowp + id), r.pl.counts ? r.sp.slot_cnt[s] : 0, r.p);
+                if (r.banned_row && ((r.banned_row[id >> 5] >> (id & 31)) & 1u)) v = -INFINITY;
+                r.sp.slot_raw[s] = div_rn(v, r.pl.t, r.pl.rt);  // from here on the final quotient
+            }
+            __syncthreads();
+        }
+        for (int i = c0 + threadIdx.x; i < c1; i += B) {
+            float x;
+            if (spec) {
+                const uint2 pair = r.sp.bits[(i - c0) >> 5];
+                const uint32_t bit = 1u << ((i - c0) & 31);
+                if (pair.x & bit) continue;
+                x = (pair.y & bit) ? -INFINITY : load_one<T>(rowp + i);
+            } else {
+                x = load_one<T>(rowp + i);
+            }
+            const float q = div_rn(x, r.pl.t, r.pl.rt);
+            if (__builtin_isnan(q)) continue;
+            f(make_entry(order_key(q), (uint32_t) i), mass_fixed(q, r.top));
+        }
+        if (spec) {
+            for (int s = threadIdx.x; s < r.sp.n_slots; s += B) {
+                const float q = r.sp.slot_raw[s];
+                if (__builtin_isnan(q)) continue;
+                f(make_entry(order_key(q), (uint32_t) r.sp.slot_id[s]), mass_fixed(q, r.top));
+            }
+        }
     }
-    for (int s = threadIdx.x; s < r.sp.n_slots; s += B) {
-        const float q = r.spec_q[s];
-        if (__builtin_isnan(q) || q == -INFINITY) continue;
-        const double w = exp((double) q - (double) r.top);
-        f(make_entry(order_key(q), (uint32_t) r.sp.slot_id[s]), (uint64_t) (w * kFix + 0.5));
-    }
+    if (spec) __syncthreads();
 }
 
 // The first entry in falling order whose running count (by_mass false) or running mass reaches `target` (strict:
 // passes it), by radix passes of 8 bits over the 64-bit entries. False when no entry does.
 template <typename T, int B>
-__device__ inline bool fb_select(const FbRow & r, bool by_mass, uint64_t target, bool strict, Select & out,
-                                 uint32_t * hist_n, unsigned long long * hist_m, int * ired) {
+__device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool strict, Select & out,
+                                 uint32_t * hist_n, unsigned long long * hist_m) {
+    int * ired = r.ired;
     Select s;
     s.prefix = 0;
     s.bits = 0;
@@ -1253,143 +1138,317 @@ __device__ inline bool fb_select(const FbRow & r, bool by_mass, uint64_t target,
     return true;
 }
 
-template <typename T>
-__global__ __launch_bounds__(kFbBlock) void fallback_kernel(Launch a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int B = kFbBlock;
+// Resolves one row the one-pass path could not finish, in the row's last work-group, with radix selects over the
+// whole row (the candidate and sort regions of LDS are free by now).
+template <typename T, int B>
+__device__ inline void fallback_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl, uint64_t low,
+                                    float top, unsigned char * lds) {
     const int tid = threadIdx.x;
-    int * ired = (int *) (lds + a.fb_off_red);
-    uint32_t * hist_n = (uint32_t *) (lds + a.fb_off_hist);
-    unsigned long long * hist_m = (unsigned long long *) (lds + a.fb_off_hist + 1024);
-    const int count = *(volatile int32_t *) &a.fb_count[0];
-    for (int li = blockIdx.x; li < count; li += gridDim.x) {
-        const int row = a.fb_rows[li];
-        FbRow r;
-        r.a = &a;
-        r.row = row;
-        r.p = a.params[row];
-        r.pl = make_plan(r.p, a.vocab, a.banned != nullptr, a.hist != nullptr);
-        r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
-        r.sp.any = false;
-        r.sp.n_slots = 0;
-        r.sp.min_banned = 0x7fffffff;
-        r.sp.max_banned = -1;
-        r.sp.bits = (uint32_t *) (lds + a.fb_off_bits);
-        r.sp.slot_id = (int32_t *) (lds + a.fb_off_slots);
-        r.sp.slot_raw = (float *) (lds + a.fb_off_slots + 4 * a.slot_cap);
-        r.sp.slot_cnt = (int32_t *) (lds + a.fb_off_slots + 8 * a.slot_cap);
-        r.spec_q = r.sp.slot_raw;
-        uint32_t bad = 0;
-        __syncthreads();
-        if (r.pl.pen || r.banned_row) {
-            r.sp.any = true;
-            build_specials<B>(r.sp, a, row, 0, a.vocab, r.pl, r.banned_row, ired, bad);
-            // the history tokens' raw logits, then their final quotients
-            for (int s = tid; s < r.sp.n_slots; s += B) {
-                const int id = r.sp.slot_id[s];
-                const float x = load_one<T>((const T *) a.logits + (int64_t) row * a.ld + id);
-                float v = penalize(x, r.pl.counts ? r.sp.slot_cnt[s] : 0, r.p);
-                if (r.banned_row && ((r.banned_row[id >> 5] >> (id & 31)) & 1u)) v = -INFINITY;
-                r.spec_q[s] = div_rn(v, r.pl.t, r.pl.rt);
-            }
-            __syncthreads();
-        }
-        const RowState rs = a.row_state[row];
-        r.top = rs.top;
-        // The total mass over the row, as the selects count it.
-        unsigned long long * tot_m = (unsigned long long *) (ired + 8);
-        if (tid == 0) *tot_m = 0;
-        __syncthreads();
-        {
-            unsigned long long mine = 0;
-            fb_visit<T, B>(r, [&](uint64_t, uint64_t w) { mine += w; });
-            atomicAdd(tot_m, mine);
-        }
-        __syncthreads();
-        const uint64_t all_m = *tot_m;
-        __syncthreads();
-        const double u = a.u[row];
-        const int fl = r.pl.flavor;
-        auto sel = [&](bool by_mass, uint64_t target, bool strict, Select & out) {
-            return fb_select<T, B>(r, by_mass, target, strict, out, hist_n, hist_m, ired);
-        };
-        // The flavor's k candidates: the k-th entry and their mass.
-        uint64_t kmass = all_m, kcount = (uint64_t) a.vocab;
-        Select sk;
-        bool have_k_entry = false;
-        if (r.pl.k < a.vocab && sel(false, (uint64_t) r.pl.k, false, sk)) {
-            kmass = sk.above_m + sk.own_m;
-            kcount = sk.above_n + 1;
-            have_k_entry = true;
-        }
-        // The kept prefix: its last entry, count and mass.
-        uint64_t kept_m = kmass, kept_n = kcount;
-        Select scut;
-        bool have_cut = false;
-        if (fl == SPX_FLAVOR_TRANSFORMERS || fl == SPX_FLAVOR_HARU) {
-            // transformers keeps the token reaching top_p (qwen3-tts/sampler.cpp:92-96); torch's zeroing in
-            // sample_token keeps the same prefix, the tokens after it weighing 0 (haru/sampler.cpp:52-59)
-            const bool applies = fl == SPX_FLAVOR_TRANSFORMERS ? r.pl.top_p < 1.0f
-                                                               : (r.pl.top_p > 0.0f && r.pl.top_p < 1.0f);
-            if (applies) {
-                const uint64_t target = (uint64_t) ((double) kmass * (double) r.pl.top_p + 0.5);
-                if (sel(true, target, false, scut) && scut.above_n + 1 <= kcount) {
-                    kept_m = scut.above_m + scut.own_m;
-                    kept_n = scut.above_n + 1;
-                    have_cut = true;
-                }
-            }
-        } else {
-            // fish-speech drops the token passing top_p, the first always kept (drama3/sampler.cpp:53-58)
-            const uint64_t target = (uint64_t) ((double) all_m * (double) r.pl.top_p + 0.5);
-            if (sel(true, target, true, scut) && scut.above_n < kcount) {
-                kept_m = scut.above_n >= 1 ? scut.above_m : scut.own_m;
-                kept_n = scut.above_n >= 1 ? scut.above_n : 1;
+    int * ired = (int *) (lds + a.off_red);
+    uint32_t * hist_n = (uint32_t *) (lds + a.off_sort);
+    unsigned long long * hist_m = (unsigned long long *) (lds + a.off_sort + 1024);
+    FbRow r;
+    r.a = &a;
+    r.row = row;
+    r.p = p;
+    r.pl = pl;
+    r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
+    r.sp.any = pl.pen || r.banned_row;
+    r.sp.n_slots = 0;
+    r.sp.bits = (uint2 *) (lds + a.off_bits);
+    r.sp.rank = (int32_t *) (lds + a.off_rank);
+    r.sp.slot_id = (int32_t *) (lds + a.off_slots);
+    r.sp.slot_raw = (float *) (lds + a.off_slots + 4 * a.slot_cap);
+    r.sp.slot_cnt = (int32_t *) (lds + a.off_slots + 8 * a.slot_cap);
+    r.top = top;
+    r.ired = ired;
+    // The total mass over the row, as the selects count it.
+    unsigned long long * tot_m = (unsigned long long *) (ired + 8);
+    if (tid == 0) *tot_m = 0;
+    __syncthreads();
+    {
+        unsigned long long mine = 0;
+        fb_visit<T, B>(r, [&](uint64_t, uint64_t w) { mine += w; });
+        atomicAdd(tot_m, mine);
+    }
+    __syncthreads();
+    const uint64_t all_m = *tot_m;
+    __syncthreads();
+    const double u = a.u[row];
+    const int fl = pl.flavor;
+    auto sel = [&](bool by_mass, uint64_t target, bool strict, Select & out) {
+        return fb_select<T, B>(r, by_mass, target, strict, out, hist_n, hist_m);
+    };
+    // The flavor's k candidates: the k-th entry and their mass.
+    uint64_t kmass = all_m, kcount = (uint64_t) a.vocab;
+    Select sk;
+    bool have_k_entry = false;
+    if (pl.k < a.vocab && sel(false, (uint64_t) pl.k, false, sk)) {
+        kmass = sk.above_m + sk.own_m;
+        kcount = sk.above_n + 1;
+        have_k_entry = true;
+    }
+    // The kept prefix: its last entry, count and mass.
+    uint64_t kept_m = kmass, kept_n = kcount;
+    Select scut;
+    bool have_cut = false;
+    if (fl == SPX_FLAVOR_TRANSFORMERS || fl == SPX_FLAVOR_HARU) {
+        // transformers keeps the token reaching top_p (qwen3-tts/sampler.cpp:92-96); torch's zeroing in
+        // sample_token keeps the same prefix, the tokens after it weighing 0 (haru/sampler.cpp:52-59)
+        const bool applies = fl == SPX_FLAVOR_TRANSFORMERS ? pl.top_p < 1.0f : (pl.top_p > 0.0f && pl.top_p < 1.0f);
+        if (applies) {
+            const uint64_t target = (uint64_t) ((double) kmass * (double) pl.top_p + 0.5);
+            if (sel(true, target, false, scut) && scut.above_n + 1 <= kcount) {
+                kept_m = scut.above_m + scut.own_m;
+                kept_n = scut.above_n + 1;
                 have_cut = true;
             }
         }
-        // pick(): the first kept entry whose running share passes u, else the last kept.
-        Select spk;
-        int id = -1;
-        const uint64_t utarget = (uint64_t) ((double) kept_m * u);
-        const bool hit = sel(true, utarget, true, spk) && spk.above_n + 1 < kept_n;
-        if (hit) {
-            id = (int) entry_id(spk.entry);
-        } else if (fl == SPX_FLAVOR_HARU) {
-            // pick() over all k weights, zeros included: the k-th token
-            id = have_k_entry ? (int) entry_id(sk.entry) : (int) ~(uint32_t) rs.low;
-        } else if (have_cut && fl == SPX_FLAVOR_TRANSFORMERS) {
-            id = (int) entry_id(scut.entry);
-        } else if (have_cut) {
-            Select sl;
-            if (sel(false, kept_n, false, sl)) id = (int) entry_id(sl.entry);
-        } else if (have_k_entry) {
-            id = (int) entry_id(sk.entry);
-        } else {
-            id = (int) ~(uint32_t) rs.low;
+    } else {
+        // fish-speech drops the token passing top_p, the first always kept (drama3/sampler.cpp:53-58)
+        const uint64_t target = (uint64_t) ((double) all_m * (double) pl.top_p + 0.5);
+        if (sel(true, target, true, scut) && scut.above_n < kcount) {
+            kept_m = scut.above_n >= 1 ? scut.above_m : scut.own_m;
+            kept_n = scut.above_n >= 1 ? scut.above_n : 1;
+            have_cut = true;
         }
-        if (tid == 0) {
-            write_row(a, row, id, SPX_ROW_OK, fl == SPX_FLAVOR_HARU ? r.pl.k : (int) kept_n);
-            if (a.out_cand_ids) {
-                // This path reports the id and the count of the kept candidates alone.
-                for (int j = 0; j < a.max_out; j++) {
-                    a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
-                    a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
-                }
+    }
+    // pick(): the first kept entry whose running share passes u, else the last kept.
+    Select spk;
+    int id = -1;
+    const uint64_t utarget = (uint64_t) ((double) kept_m * u);
+    const bool hit = sel(true, utarget, true, spk) && spk.above_n + 1 < kept_n;
+    if (hit) {
+        id = (int) entry_id(spk.entry);
+    } else if (fl == SPX_FLAVOR_HARU) {
+        // pick() over all k weights, zeros included: the k-th token
+        id = have_k_entry ? (int) entry_id(sk.entry) : (int) ~(uint32_t) low;
+    } else if (have_cut && fl == SPX_FLAVOR_TRANSFORMERS) {
+        id = (int) entry_id(scut.entry);
+    } else if (have_cut) {
+        Select sl;
+        if (sel(false, kept_n, false, sl)) id = (int) entry_id(sl.entry);
+    } else if (have_k_entry) {
+        id = (int) entry_id(sk.entry);
+    } else {
+        id = (int) ~(uint32_t) low;
+    }
+    if (tid == 0) {
+        write_row(a, row, id, SPX_ROW_OK, fl == SPX_FLAVOR_HARU ? pl.k : (int) kept_n);
+        if (a.out_cand_ids) {
+            // This path reports the id and the count of the kept candidates alone.
+            for (int j = 0; j < a.max_out; j++) {
+                a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
+                a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
             }
         }
-        __syncthreads();
+        atomicAdd(a.fb_count, 1);  // rows this path has resolved since the handle was made
     }
-    // The last work-group to finish clears the list for the next launch, after every work-group has read its count.
+}
+
+template <typename T>
+__global__ __launch_bounds__(kBlock) void stream_kernel(Launch a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int B = kBlock;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    int row, split;
+    xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
+    if (row >= a.rows) return;
+
+    spx_row_params p;
+    if (a.params) {
+        p = a.params[row];
+    } else {
+        // spx_argmax_rows: std::max_element of the suppressed logits
+        p.flavor = SPX_FLAVOR_TRANSFORMERS;
+        p.greedy = 1;
+        p.temperature = 1.0f;
+        p.top_k = 0;
+        p.top_p = 1.0f;
+        p.repetition_penalty = 1.0f;
+        p.presence_penalty = 0.0f;
+        p.frequency_penalty = 0.0f;
+    }
+    const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr);
+    const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
+    const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
+    const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
+
+    int * ired = (int *) (lds + a.off_red);
+    double * dred = (double *) (lds + a.off_red + 256);
+    uint64_t * red64 = (uint64_t *) (lds + a.off_red + 512);
+    float * fred = (float *) (lds + a.off_red + 768);
+    uint32_t * ured = (uint32_t *) (lds + a.off_red + 1024);
+    int * wave_n = (int *) (lds + a.off_red + 1088);
+    uint64_t * wave_thr = (uint64_t *) (lds + a.off_red + 1152);
+    uint32_t * wg_tau = (uint32_t *) (ired + 60);  // the largest K-th key any wave has published
+
+    Lane ln;
+    lane_init(ln);
+    Specials sp;
+    sp.any = false;
+    sp.n_slots = 0;
+    sp.bits = (uint2 *) (lds + a.off_bits);
+    sp.rank = (int32_t *) (lds + a.off_rank);
+    sp.slot_id = (int32_t *) (lds + a.off_slots);
+    sp.slot_raw = (float *) (lds + a.off_slots + 4 * a.slot_cap);
+    sp.slot_cnt = (int32_t *) (lds + a.off_slots + 8 * a.slot_cap);
+    uint32_t bad = 0;
+    if (tid == 0) *wg_tau = 0;
+    if (pl.mode != kInvalid && (pl.pen || banned_row)) {
+        sp.any = true;
+        build_specials<B>(sp, a, row, c0, c1, pl, banned_row, ired, bad);
+    }
     __syncthreads();
-    if (tid == 0) {
-        __threadfence();
-        const int done = atomicAdd(&a.fb_count[1], 1);
-        if (done == (int) gridDim.x - 1) {
-            a.fb_count[2] = a.fb_count[0];  // kept for spx_sampler_last_stats
-            a.fb_count[0] = 0;
-            a.fb_count[1] = 0;
+    ln.flags |= bad;
+
+    const bool sampling = pl.mode == kTopK || pl.mode == kFull;
+    WaveBuf wb;
+    wb.buf = (uint64_t *) (lds + a.off_cand) + wave * kCap;
+    wb.n = 0;
+    wb.thr = 0;
+    wb.thr_key = 0;
+    wb.K = pl.kc;
+
+    if (pl.mode != kInvalid) {
+        stream_chunk<T, B>(a, rowp, c0, c1, pl, sp, ln, wb, wg_tau);
+        // Token 0, where it is not a history token, for std::max_element's NaN in front.
+        if (c0 == 0 && tid == 0) {
+            const uint2 pair = sp.any ? sp.bits[0] : make_uint2(0u, 0u);
+            if (!(pair.x & 1u)) {
+                const float x0 = (pair.y & 1u) ? -INFINITY : load_one<T>(rowp);
+                if (__builtin_isnan(x0)) ln.flags |= kNaN0;
+            }
         }
+        if (sp.any) {
+            __syncthreads();
+            take_specials<B>(p, pl, sp, banned_row, ln, wb, wg_tau);
+        }
+    }
+
+    // Each wave keeps exactly its top K; its K-th entry bounds the row's K-th from below.
+    uint64_t thr = 0;
+    if (sampling) {
+        if (wb.n > wb.K) {
+            thr = wave_compact(wb.buf, &wb.n, wb.K);
+        } else if (wb.n == wb.K) {
+            uint64_t m = ~0ull;
+            for (int i = lane; i < wb.n; i += kWave) m = wb.buf[i] < m ? wb.buf[i] : m;
+            thr = wave_min_u64(m);
+        }
+    }
+    if (lane == 0) {
+        wave_n[wave] = sampling ? wb.n : 0;
+        wave_thr[wave] = thr;
+    }
+    const RowTotals tot = reduce_lanes<B>(ln, red64, dred, fred, ured);  // its barriers publish wave_n
+
+    uint64_t * sorted = (uint64_t *) (lds + a.off_sort);
+    int n = 0;
+    bool complete = true;
+    if (sampling) {
+        n = union_and_sort<B>((uint64_t *) (lds + a.off_cand), wave_n, wave_thr, sorted, a.sort_cap, ired);
+        complete = n < pl.kc;  // fewer than K: no wave ever dropped an entry
+        n = min(n, pl.kc);
+    }
+
+    FinishLds L;
+    L.w = (double *) (lds + a.off_cand);
+    L.red = dred;
+    L.ired = ired;
+    L.pf = (float *) (lds + a.off_cand + 8 * kKeep);
+
+    if (a.splits > 1) {
+        // Publish this chunk's partial; the last chunk of the row to arrive merges them.
+        Partial * part = a.partials + (int64_t) row * a.splits + split;
+        uint64_t * pc = a.part_cands + ((int64_t) row * a.splits + split) * kKeep;
+        for (int i = tid; i < n; i += B) pc[i] = sorted[i];
+        if (tid == 0) {
+            part->best = tot.best;
+            part->low = tot.low;
+            part->s = tot.s;
+            part->m = tot.m;
+            part->mx = tot.mx;
+            part->mn = tot.mn;
+            part->flags = tot.flags;
+            part->n = n;
+            part->complete = complete ? 1 : 0;
+            part->kth = (n >= pl.kc && n > 0) ? sorted[n - 1] : 0;
+        }
+        // One wave makes the partial visible device-wide and counts the chunk in; the last chunk's first wave makes
+        // the others' visible to its work-group.
+        __syncthreads();
+        if (tid == 0) {
+            __threadfence();
+            const unsigned prev = atomicAdd(&a.counters[row], 1u);
+            const int last = prev == (unsigned) (a.splits - 1);
+            if (last) {
+                __threadfence();
+                a.counters[row] = 0;  // ready for the next launch
+            }
+            ired[0] = last;
+        }
+        __syncthreads();
+        if (!ired[0]) return;
+        RowTotals t;
+        t.best = 0;
+        t.low = ~0ull;
+        t.flags = 0;
+        t.m = -FLT_MAX;
+        t.mx = -INFINITY;
+        t.mn = INFINITY;
+        t.s = 0;
+        uint64_t floor = 0;
+        bool all_complete = true;
+        const Partial * pr = a.partials + (int64_t) row * a.splits;
+        for (int s2 = 0; s2 < a.splits; s2++) {
+            const Partial q = pr[s2];
+            t.best = q.best > t.best ? q.best : t.best;
+            t.low = q.low < t.low ? q.low : t.low;
+            t.flags |= q.flags;
+            t.m = fmaxf(t.m, q.m);
+            t.mx = fmaxf(t.mx, q.mx);
+            t.mn = fminf(t.mn, q.mn);
+            floor = q.kth > floor ? q.kth : floor;
+            all_complete = all_complete && q.complete;
+        }
+        for (int s2 = 0; s2 < a.splits; s2++) {
+            const Partial q = pr[s2];
+            t.s += q.s * ((q.m == t.m) ? 1.0 : exp((double) q.m - (double) t.m));
+        }
+        int total = 0;
+        if (sampling) {
+            for (int s2 = 0; s2 < a.splits; s2++) {
+                const int ns = pr[s2].n;
+                const uint64_t * src = a.part_cands + ((int64_t) row * a.splits + s2) * kKeep;
+                for (int i0 = 0; i0 < ns; i0 += B) {
+                    const int i = i0 + tid;
+                    const bool keep = i < ns && src[i] >= floor;
+                    int cnt_total;
+                    const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, ired + 32, cnt_total);
+                    if (keep && total + pos < a.sort_cap) sorted[total + pos] = src[i];
+                    total += cnt_total;
+                }
+            }
+            total = min(total, a.sort_cap);
+            int np2 = 1;
+            while (np2 < total) np2 <<= 1;
+            for (int i = total + tid; i < np2; i += B) sorted[i] = 0;
+            __syncthreads();
+            block_sort_desc<B>(sorted, np2);
+        }
+        n = min(total, pl.kc);
+        if (!finish_row<B>(a, row, p, pl, t, sorted, n, all_complete, L)) {
+            const float top = entry_value(sorted[0]);
+            __syncthreads();
+            fallback_row<T, B>(a, row, p, pl, t.low, top, lds);
+        }
+        return;
+    }
+    if (!finish_row<B>(a, row, p, pl, tot, sorted, n, complete, L)) {
+        const float top = entry_value(sorted[0]);
+        __syncthreads();
+        fallback_row<T, B>(a, row, p, pl, tot.low, top, lds);
     }
 }
 
@@ -1407,26 +1466,12 @@ hipError_t launch_stream(const Launch & a, hipStream_t s) {
     return hipGetLastError();
 }
 
-hipError_t launch_fallback(const Launch & a, int grid, hipStream_t s) {
-    if (a.dtype == SPX_BF16) {
-        hipLaunchKernelGGL(fallback_kernel<uint16_t>, dim3(grid), dim3(kFbBlock), a.fb_lds_bytes, s, a);
-    } else {
-        hipLaunchKernelGGL(fallback_kernel<float>, dim3(grid), dim3(kFbBlock), a.fb_lds_bytes, s, a);
-    }
-    return hipGetLastError();
-}
-
-hipError_t set_lds_limits(int stream_bytes, int fb_bytes) {
+hipError_t set_lds_limits(int stream_bytes) {
     hipError_t e = hipSuccess;
     if (stream_bytes > 65536) {
         e = hipFuncSetAttribute((const void *) stream_kernel<float>, hipFuncAttributeMaxDynamicSharedMemorySize, stream_bytes);
         if (e == hipSuccess)
             e = hipFuncSetAttribute((const void *) stream_kernel<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, stream_bytes);
-    }
-    if (e == hipSuccess && fb_bytes > 65536) {
-        e = hipFuncSetAttribute((const void *) fallback_kernel<float>, hipFuncAttributeMaxDynamicSharedMemorySize, fb_bytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *) fallback_kernel<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, fb_bytes);
     }
     return e;
 }
