@@ -17,6 +17,7 @@ struct spx_sampler {
     int cus = 256;
     void * ws = nullptr;
     spx::Launch base{};
+    int last_block = 0, last_splits = 0;
 };
 
 namespace {
@@ -34,45 +35,57 @@ spx_status hip_fail(hipError_t e, const char * what) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// The bytes of the LDS regions of the special tokens of a chunk of `chunk` tokens: two bit words and a rank per 32.
-size_t bits_bytes(int chunk) {
-    const size_t words = (size_t) (chunk + 31) / 32;
-    return align_up(words * 8, 16) + align_up(words * 4, 16);
-}
-
-// Lays out both kernels' LDS and the launch shape for one call.
-void plan_launch(const spx_sampler * s, spx::Launch & a, bool greedy_only, bool has_hist, bool has_ban) {
+// The launch shape and the kernel's LDS layout for one call: the control block, reduction scratch, the chunk's
+// special-token words, the history slots (index, rank, count, captured vector), the candidate buffer and the sorted
+// candidates (also the multi-pass path's radix histograms).
+size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool has_hist, bool has_ban, int max_hist) {
     using namespace spx;
-    // Work-groups per row: enough chunks to give the CUs about four work-groups each, but chunks of at least 4096
-    // tokens, and few enough that the last chunk can merge them all.
-    const int max_splits = greedy_only ? kMaxSplitsGreedy : kMaxSplits;
-    int splits = std::max(1, (4 * s->cus + a.rows - 1) / std::max(a.rows, 1));
-    splits = std::min(splits, max_splits);
-    splits = std::min(splits, std::max(1, a.vocab / 4096));
-    int chunk = (a.vocab + splits - 1) / splits;
-    chunk = (int) align_up((size_t) chunk, 64);
-    splits = (a.vocab + chunk - 1) / chunk;
-    a.splits = splits;
-    a.chunk = chunk;
-    a.nwg = a.rows * splits;
-    a.sort_cap = kSortCap;
-    a.slot_cap = has_hist ? s->max_hist : 0;
-
     size_t off = 0;
+    a.off_ctl = (int) off;
+    off += 1024;
     a.off_red = (int) off;
     off += 1280;
     const size_t words = (size_t) (chunk + 31) / 32;
-    a.off_bits = (int) off;
+    a.off_spec = (int) off;
     if (has_hist || has_ban) off += align_up(words * 8, 16);
-    a.off_rank = (int) off;
-    if (has_hist || has_ban) off += align_up(words * 4, 16);
-    a.off_slots = (int) off;
-    off += align_up((size_t) a.slot_cap * 12, 16);
+    const size_t slots = has_hist ? (size_t) max_hist : 0;
+    a.off_meta = (int) off;
+    off += align_up(slots * 4, 16);
+    a.off_ufirst = (int) off;
+    off += align_up(slots * 4, 16);
+    a.off_cnt = (int) off;
+    off += align_up(slots * 4, 16);
+    a.off_cap = (int) off;
+    off += slots * 16;
+    a.cand_cap = 2 * block;
     a.off_cand = (int) off;
-    if (!greedy_only) off += (size_t) kWaves * kCap * 8;
+    if (!greedy_only) off += (size_t) a.cand_cap * 8;
     a.off_sort = (int) off;
     if (!greedy_only) off += (size_t) kSortCap * 8;
     a.lds_bytes = (int) off;
+    return off;
+}
+
+void plan_launch(spx_sampler * s, spx::Launch & a, bool greedy_only, bool has_hist, bool has_ban) {
+    using namespace spx;
+    const int block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
+    // Chunks per row: about one work-group of 1024 threads, or four of 256, per CU; chunks of at least one step of the
+    // work-group, and few enough that the row's last chunk can merge them.
+    const int per_cu = block == kBlockBig ? 1 : 4;
+    const int max_splits = greedy_only ? kMaxSplitsGreedy : kMaxSplits;
+    int splits = std::max(1, (per_cu * s->cus + a.rows - 1) / std::max(a.rows, 1));
+    splits = std::min(splits, max_splits);
+    splits = std::min(splits, std::max(1, a.vocab / (kE * block)));
+    int chunk = (a.vocab + splits - 1) / splits;
+    chunk = (int) align_up((size_t) chunk, 64);
+    splits = (a.vocab + chunk - 1) / chunk;
+    a.block = block;
+    a.splits = splits;
+    a.chunk = chunk;
+    a.nwg = a.rows * splits;
+    plan_lds(a, block, chunk, greedy_only, has_hist, has_ban, s->max_hist);
+    s->last_block = block;
+    s->last_splits = splits;
 }
 
 spx_status check_common(spx_sampler * s, const void * logits, int dtype, int rows, int vocab, int64_t ld,
@@ -115,9 +128,14 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
         s->cus = cus;
+    if (max_hist > kMaxHist) {
+        delete s;
+        return fail(SPX_ERR_INVALID_ARGUMENT, "max_hist above 4096");
+    }
     // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary.
-    const size_t slot_bytes = align_up((size_t) max_hist * 12, 16);
-    const size_t lds_max = 1280 + bits_bytes(max_vocab) + slot_bytes + (size_t) kWaves * kCap * 8 + (size_t) kSortCap * 8;
+    Launch probe{};
+    const int block = max_vocab >= kBigVocab ? kBlockBig : kBlockSmall;
+    const size_t lds_max = plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist);
     if (lds_max > 160 * 1024) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
@@ -198,8 +216,8 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_cand_probs = d_out_cand_probs;
     a.max_out = d_out_cand_ids ? s->max_out : 0;
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
-    hipError_t e = spx::launch_stream(a, (hipStream_t) stream);
-    if (e != hipSuccess) return hip_fail(e, "stream_kernel launch");
+    hipError_t e = spx::launch_sampler(a, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
 }
 
@@ -229,8 +247,8 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_cand_probs = nullptr;
     a.max_out = 0;
     plan_launch(s, a, true, false, d_banned != nullptr);
-    hipError_t e = spx::launch_stream(a, (hipStream_t) stream);
-    if (e != hipSuccess) return hip_fail(e, "stream_kernel launch");
+    hipError_t e = spx::launch_sampler(a, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
 }
 
@@ -240,8 +258,8 @@ spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {
     hipError_t e = hipMemcpy(&c, s->base.fb_count, sizeof(c), hipMemcpyDeviceToHost);
     if (e != hipSuccess) return hip_fail(e, "hipMemcpy");
     out->rows_fallback = c;
-    out->splits = 0;
-    out->block = spx::kBlock;
+    out->splits = s->last_splits;
+    out->block = s->last_block;
     out->reserved = 0;
     return SPX_OK;
 }

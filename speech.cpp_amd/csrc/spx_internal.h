@@ -1,4 +1,4 @@
-// spx_internal.h — what the host side of the sampler and its kernels share: the launch record, the workspace records
+// spx_internal.h — what the host side of the sampler and its kernel share: the launch record, the workspace records
 // and the fixed sizes of the one-pass path.
 #pragma once
 
@@ -8,33 +8,37 @@
 
 namespace spx {
 
-// Threads per work-group.
-constexpr int kBlock = 256;
-constexpr int kWaves = kBlock / 64;
-// Entries a wave keeps: the top-k of a row with top_k <= kKeep, and the top kKeep of a row drawing over more
-// (its top-p set must end within them, or the row takes the multi-pass path).
+// Threads per work-group: 1024 for rows of at least kBigVocab tokens (one work-group per CU streams a whole row),
+// 256 below.
+constexpr int kBlockBig = 1024;
+constexpr int kBlockSmall = 256;
+constexpr int kBigVocab = 16384;
+// Final logits each lane holds per step of the stream (four 16-byte vectors of fp32, two of bf16).
+constexpr int kE = 16;
+// The top-k of a row with top_k <= kKeep is held exactly; a row drawing over more tokens holds at least its top
+// kKeepFull (its top-p set must end within what is held, or the row takes the multi-pass path).
 constexpr int kKeep = 256;
-// Entries a wave keeps for a row drawing over more than kKeep tokens.
 constexpr int kKeepFull = 128;
-// A wave's buffer: its kKeep best plus one offer of 64 lanes x 4 elements before it must compact.
-constexpr int kCap = 512;
-constexpr int kPerLane = kCap / 64;
-// Entries the last chunk of a row can merge: kKeep from each of at most kMaxSplits chunks.
+// Entries one chunk's sorted candidates can hold, and the merge of kMaxSplits chunks of kKeep each.
+constexpr int kSortCap = 1024;
 constexpr int kMaxSplits = 4;
 constexpr int kMaxSplitsGreedy = 16;
-constexpr int kSortCap = 1024;  // >= kWaves * kKeep and >= kMaxSplits * kKeep, a power of two
+// Buckets of the histogram that raises a chunk's threshold.
+constexpr int kBuckets = 128;
+// The largest history a handle takes: slot ranks are kept in 24 bits and the LDS must hold the slots.
+constexpr int kMaxHist = 4096;
 
 // What a chunk of a row leaves for the last chunk of its row.
 struct Partial {
-    uint64_t best;     // greedy: the largest entry of the final logits (0: none)
-    uint64_t low;      // the last token of the order
-    double s;          // sum of exp(q - m)
+    uint64_t best;     // greedy: the largest entry of the final logits (0: none above -inf)
+    uint64_t floor;    // every entry of the chunk at or above it is among those published
+    double s;          // sum of exp(q - m) over the chunk
     float m;
-    float mx, mn;      // range of the final logits
     uint32_t flags;
     int32_t n;         // sorted entries published
-    int32_t complete;  // 1 when the chunk's every valid token is among them
-    uint64_t kth;      // its K-th entry (0 when it holds fewer than K)
+    int32_t complete;  // 1 when they are every valid token of the chunk
+    int32_t broken;    // 1 when the chunk could not keep its candidates (the row takes the multi-pass path)
+    int32_t pad;
 };
 
 struct Launch {
@@ -44,7 +48,6 @@ struct Launch {
     const int32_t * hist;
     const int32_t * hist_off;
     int max_hist;
-    int slot_cap;
     const uint32_t * banned;
     int64_t banned_stride;
     const spx_row_params * params;
@@ -55,10 +58,10 @@ struct Launch {
     int32_t * out_cand_ids;
     float * out_cand_probs;
     int max_out;
-    int splits, chunk, nwg;
-    int sort_cap;
-    // LDS layout (byte offsets). The multi-pass path keeps its radix histograms in the sort region.
-    int off_bits, off_rank, off_slots, off_cand, off_sort, off_red, lds_bytes;
+    int block, splits, chunk, nwg;
+    int cand_cap;  // entries of a chunk's candidate buffer
+    // LDS layout (byte offsets)
+    int off_ctl, off_red, off_spec, off_meta, off_ufirst, off_cnt, off_cap, off_cand, off_sort, lds_bytes;
     // workspace
     uint32_t * counters;   // [max_rows], each back to 0 after its row's last chunk
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]
@@ -71,6 +74,6 @@ struct Launch {
 #include <hip/hip_runtime.h>
 
 namespace spx {
-hipError_t launch_stream(const Launch & a, hipStream_t s);
-hipError_t set_lds_limits(int stream_bytes);
+hipError_t launch_sampler(const Launch & a, hipStream_t s);
+hipError_t set_lds_limits(int bytes);
 }  // namespace spx

@@ -1,19 +1,23 @@
-// spx_kernels.hip — the gfx950 kernels of the batched token sampler.
+// spx_kernels.hip — the gfx950 kernel of the batched token sampler.
 //
-// One launch of stream_kernel samples a batch. Each work-group takes one chunk of one row (a row is cut into
-// `splits` chunks so that small batches still fill the 256 CUs), reads its logits once from HBM with 16-byte loads,
-// and keeps on chip only what the draw needs:
-//   - the row's special tokens (history ids, banned ids) as an LDS bitmap over the chunk plus a sorted slot list, so
-//     the penalty arithmetic runs once per special token instead of once per logit;
-//   - the exact quotient l/T of every logit (Markstein's correction, correctly rounded like the reference's division);
-//   - an online (max, sum of exp) pair per thread, summed in double, for the rows whose normalization spans the whole
-//     vocabulary (top-k off, or the FISH flavor);
-//   - per wave, a buffer of the best entries (key, id) seen so far with a rising threshold: each compaction keeps the
-//     wave's exact top K, so the union over waves holds the row's top K without a sort of the row.
-// The last work-group of a row (an atomic counter per row, reset by that work-group) merges the chunks' partial
-// results, sorts the few hundred surviving entries in LDS and applies the flavor's rule: softmax weights in double,
-// the top-p cut, and pick() with the row's uniform. A row whose top-p set runs beyond the entries kept is resolved
-// by that same work-group with radix selects over (count, mass) histograms of the whole row.
+// One launch samples a batch. Each work-group takes one chunk of one row (a row is cut into `splits` chunks when the
+// batch alone would not fill the CUs) and reads the chunk's logits once, 16 bytes per lane per load with the next
+// step's loads in flight. Per step every lane holds 16 logits in registers and keeps, for the whole chunk:
+//   - the exact quotient q = l/t of each logit (Markstein's correction step, correctly rounded like the reference's
+//     float division), and the sum of exp(q - m) as one fma, one exp2 and one add per logit against a wave-uniform
+//     reference m, corrected exactly for the rounding of m*log2(e) at the end;
+//   - every token whose quotient reaches the chunk's threshold tau, appended to one candidate buffer in LDS. tau
+//     starts at a bound taken from the first step's lane maxima (at least K tokens lie above it) and rises from a
+//     128-bucket histogram of the appended quotients, so appends become rare after the first steps;
+//   - the special tokens (a penalized row's history and the banned ids) as a bitmap in LDS: they are masked to -inf
+//     with two bit operations per logit, and a history token's raw logit is captured for the penalty stage, which
+//     runs on the few hundred history tokens after the stream.
+// A logit whose term is not finite (NaN, infinities, a quotient out of range) sends its group of 16 to an exact path
+// that sets the flags the reference's checks read. After the stream the chunk's candidates at or above the final
+// tau are sorted and the row is finished by the flavor's rule (softmax weights in double, top-k/top-p, pick() with
+// the row's uniform) - by the chunk itself, or by the last chunk of the row to arrive, which merges the others'. A
+// row whose draw runs past the candidates held, or whose flags need every token, is resolved by the multi-pass path
+// (exact radix selects over the whole row) in that same work-group.
 //
 // Citations are relative to the reference checkout (nyosegawa/speech.cpp 0.11.1).
 
@@ -27,6 +31,9 @@
 
 namespace spx {
 
+constexpr float kL2e = 1.4426950408889634f;  // log2(e), rounded to float
+constexpr uint32_t kNegInfBits = 0xff800000u;
+
 // ------------------------------------------------------------------------------------------------------------------
 // Row plans
 // ------------------------------------------------------------------------------------------------------------------
@@ -35,23 +42,27 @@ enum Mode : int { kGreedy = 0, kTopK = 1, kFull = 2, kInvalid = 3 };
 
 enum Flag : uint32_t {
     kNaN = 1u,        // a NaN among the final logits
-    kTempOver = 8u,   // HARU: a finite logit whose quotient is not finite (src/families/haru/sampler.cpp:34)
+    kPosInf = 2u,     // a final logit is +inf
+    kFinite = 4u,     // a final logit is finite
+    kTempOver = 8u,   // a finite final logit whose quotient is not finite (src/families/haru/sampler.cpp:33-35)
     kNaN0 = 16u,      // the final logit of token 0 is NaN (std::max_element then answers 0)
+    kNegInf = 32u,    // a final logit of a token that is not banned is -inf
     kBadHist = 64u,   // the row's history is longer than the handle was created for
 };
 
 struct Plan {
     int mode;
     int flavor;
-    int k;          // the flavor's top-k count: the candidates the reference sorts
-    int kc;         // entries kept per wave: min(k, kKeep) for top-k rows, kKeep for full rows
-    float t;        // the divisor of the flavor
-    float rt;       // 1/t rounded
+    int k;        // the flavor's top-k count: the candidates the reference sorts
+    int K;        // entries held at least: k for a top-k row, kKeepFull for a row drawing over more
+    float t;      // the divisor of the flavor
+    float rt;     // 1/t rounded
     float top_p;
-    bool need_s;    // sum of exp over the whole vocabulary
-    bool need_low;  // the last token in the order, for a draw over the whole vocabulary
-    bool pen;       // penalties read the history
-    bool counts;    // presence or frequency: the history's counts
+    bool need_s;  // sum of exp over the whole vocabulary
+    bool pen;     // penalties read the history
+    bool counts;  // the frequency penalty: the history's counts
+    bool xmin;    // greedy FISH: track the smallest raw logit (its -inf check)
+    bool nanchk;  // greedy: look for NaN among the final logits
 };
 
 __device__ inline bool neutral(const spx_row_params & p) {
@@ -63,13 +74,14 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
     pl.flavor = p.flavor;
     pl.top_p = p.top_p;
     pl.pen = !neutral(p) && has_hist;
-    pl.counts = pl.pen && (p.presence_penalty != 0.0f || p.frequency_penalty != 0.0f);
+    pl.counts = pl.pen && p.frequency_penalty != 0.0f;
     pl.need_s = false;
-    pl.need_low = false;
     pl.k = 1;
-    pl.kc = 1;
+    pl.K = 1;
     pl.t = 1.0f;
     pl.rt = 1.0f;
+    pl.xmin = false;
+    pl.nanchk = false;
     bool bad = p.flavor < SPX_FLAVOR_TRANSFORMERS || p.flavor > SPX_FLAVOR_FISH;
     bad = bad || __builtin_isnan(p.temperature) || __builtin_isnan(p.top_p) ||
           __builtin_isnan(p.repetition_penalty) || __builtin_isnan(p.presence_penalty) ||
@@ -85,6 +97,8 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
     }
     if (p.greedy || (p.flavor == SPX_FLAVOR_HARU && p.temperature <= 0.0f)) {
         pl.mode = kGreedy;
+        pl.nanchk = p.flavor != SPX_FLAVOR_TRANSFORMERS;
+        pl.xmin = p.flavor == SPX_FLAVOR_FISH;
         return pl;
     }
     int k;
@@ -94,17 +108,9 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
     pl.k = k;
     pl.t = p.flavor == SPX_FLAVOR_FISH ? fmaxf(p.temperature, 1e-5f) : p.temperature;
     pl.rt = 1.0f / pl.t;
-    if (k <= kKeep) {
-        pl.mode = kTopK;
-        pl.kc = k;
-    } else {
-        pl.mode = kFull;
-        pl.kc = kKeepFull;
-    }
+    pl.mode = k <= kKeep ? kTopK : kFull;
+    pl.K = pl.mode == kTopK ? k : kKeepFull;
     pl.need_s = pl.mode == kFull || p.flavor == SPX_FLAVOR_FISH;
-    // The last token of a draw over every token: pick() returns it where u passes every cumulative share.
-    pl.need_low = pl.mode == kFull && k == vocab &&
-                  (p.flavor == SPX_FLAVOR_HARU || !(p.top_p < 1.0f));
     return pl;
 }
 
@@ -119,9 +125,28 @@ __device__ inline float penalize(float x, int count, const spx_row_params & p) {
     return x;
 }
 
+__device__ __forceinline__ float uniform_f(float v) {
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
+}
+
+// v, or -inf where bit k of `kill` is set: a sign-extended bit field and a bitfield insert.
+__device__ __forceinline__ float kill_to(float v, uint32_t kill, int k) {
+    const uint32_t mk = (uint32_t) __builtin_amdgcn_sbfe((int) kill, k, 1);
+    return __uint_as_float((mk & kNegInfBits) | (~mk & __float_as_uint(v)));
+}
+
 // ------------------------------------------------------------------------------------------------------------------
-// Block-wide helpers (kBlock threads)
+// Work-group helpers
 // ------------------------------------------------------------------------------------------------------------------
+
+// LDS scratch of the reductions.
+struct Red {
+    int i[64];
+    double d[32];
+    uint64_t u[32];
+    float f[64];
+    uint32_t w[32];
+};
 
 template <int B>
 __device__ inline int block_excl_scan_i32(int v, int * red, int & total) {
@@ -167,7 +192,7 @@ __device__ inline double block_incl_scan_f64(double v, double * red) {
 template <int B>
 __device__ inline int block_min_i32(int v, int * red) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
-    for (int m = 32; m >= 1; m >>= 1) v = min(v, __shfl_xor(v, m, kWave));
+    v = (int) wave_reduce_u32((uint32_t) v, [](uint32_t a, uint32_t b) { return (int) a < (int) b ? a : b; });
     if (lane == 0) red[wave] = v;
     __syncthreads();
     int t = red[0];
@@ -176,7 +201,55 @@ __device__ inline int block_min_i32(int v, int * red) {
     return t;
 }
 
-// Sorts a[0..n) (n a power of two, n <= 2*B*8) into falling order, in LDS.
+template <int B>
+__device__ inline uint32_t block_or_u32(uint32_t v, uint32_t * red) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    v = wave_or_u32(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    uint32_t t = 0;
+    for (int w = 0; w < B / kWave; w++) t |= red[w];
+    __syncthreads();
+    return t;
+}
+
+template <int B>
+__device__ inline float block_max_f32(float v, float * red) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    v = wave_max_f32(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = -INFINITY;
+    for (int w = 0; w < B / kWave; w++) t = fmaxf(t, red[w]);
+    __syncthreads();
+    return t;
+}
+
+template <int B>
+__device__ inline uint64_t block_max_u64(uint64_t v, uint64_t * red) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    v = wave_max_u64(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    uint64_t t = 0;
+    for (int w = 0; w < B / kWave; w++) t = red[w] > t ? red[w] : t;
+    __syncthreads();
+    return t;
+}
+
+template <int B>
+__device__ inline uint64_t block_min_u64(uint64_t v, uint64_t * red) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    v = wave_min_u64(v);
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    uint64_t t = ~0ull;
+    for (int w = 0; w < B / kWave; w++) t = red[w] < t ? red[w] : t;
+    __syncthreads();
+    return t;
+}
+
+// Sorts a[0..n) (n a power of two) into falling order, in LDS.
 template <int B>
 __device__ inline void block_sort_desc(uint64_t * a, int n) {
     for (int size = 2; size <= n; size <<= 1) {
@@ -196,153 +269,63 @@ __device__ inline void block_sort_desc(uint64_t * a, int n) {
     }
 }
 
-// ------------------------------------------------------------------------------------------------------------------
-// The wave's candidate buffer
-// ------------------------------------------------------------------------------------------------------------------
-
-// Number of set predicates over the wave.
-__device__ __forceinline__ int wave_count(bool p) { return (int) __popcll(ballot(p)); }
-
-// The K-th largest entry of the n entries the wave holds in v[] (kPerLane per lane, 0 for none), 1 <= K <= n. The
-// counts of each step are ballots, so the search stays in scalar registers.
-__device__ __forceinline__ uint64_t wave_kth_largest(const uint64_t (&v)[kPerLane], int K) {
-    // First the K-th largest key (the high word), by a bitwise search from the highest bit where keys differ.
-    uint32_t hi = 0, lo = 0xffffffffu;
-#pragma unroll
-    for (int j = 0; j < kPerLane; j++) {
-        if (v[j]) {
-            hi = max(hi, entry_key(v[j]));
-            lo = min(lo, entry_key(v[j]));
-        }
-    }
-    hi = wave_max_u32(hi);
-    lo = wave_min_u32(lo);
-    uint32_t key = hi;
-    if (hi != lo) {
-        const int top = 31 - __builtin_clz(hi ^ lo);
-        key = hi & ~((top == 31) ? 0xffffffffu : ((2u << top) - 1u));
-        for (int b = top; b >= 0; b--) {
-            const uint32_t c = key | (1u << b);
-            int cnt = 0;
-#pragma unroll
-            for (int j = 0; j < kPerLane; j++) cnt += wave_count(v[j] != 0 && entry_key(v[j]) >= c);
-            if (cnt >= K) key = c;
-        }
-    }
-    // Entries above that key, and the ties at it.
-    int gt = 0, eq = 0;
-#pragma unroll
-    for (int j = 0; j < kPerLane; j++) {
-        gt += wave_count(v[j] != 0 && entry_key(v[j]) > key);
-        eq += wave_count(v[j] != 0 && entry_key(v[j]) == key);
-    }
-    const int need = K - gt;  // 1 <= need <= eq
-    // Among the ties, the need-th largest low word (the lowest ids come first).
-    uint32_t lw;
-    if (need == eq) {
-        uint32_t m = 0xffffffffu;
-#pragma unroll
-        for (int j = 0; j < kPerLane; j++) {
-            if (v[j] != 0 && entry_key(v[j]) == key) m = min(m, (uint32_t) v[j]);
-        }
-        lw = wave_min_u32(m);
-    } else {
-        lw = 0;
-        for (int b = 31; b >= 0; b--) {
-            const uint32_t c = lw | (1u << b);
-            int cnt = 0;
-#pragma unroll
-            for (int j = 0; j < kPerLane; j++) cnt += wave_count(v[j] != 0 && entry_key(v[j]) == key && (uint32_t) v[j] >= c);
-            if (cnt >= need) lw = c;
-        }
-    }
-    return ((uint64_t) key << 32) | lw;
-}
-
-// Keeps the wave's top K of its n entries (exactly K), in buf[0..K); returns the K-th, the new threshold. Out of
-// line: it runs a few times per wave and row.
-__device__ __attribute__((noinline)) uint64_t wave_compact(uint64_t * buf, int * n, int K) {
-    uint64_t v[kPerLane];
-    const int lane = lane_id();
-    const int cnt = *n;
-#pragma unroll
-    for (int j = 0; j < kPerLane; j++) {
-        const int i = lane + kWave * j;
-        v[j] = i < cnt ? buf[i] : 0;
-    }
-    const uint64_t kth = wave_kth_largest(v, K);
-    int pos = 0;
-#pragma unroll
-    for (int j = 0; j < kPerLane; j++) {
-        const bool keep = v[j] != 0 && v[j] >= kth;
-        const uint64_t m = ballot(keep);
-        if (keep) buf[pos + lanes_below(m)] = v[j];
-        pos += __popcll(m);
-    }
-    *n = pos;
-    return kth;
-}
-
-struct WaveBuf {
-    uint64_t * buf;
-    int n;            // entries held (wave-uniform)
-    uint64_t thr;     // entries must exceed this to enter
-    uint32_t thr_key; // its key: the fast test
-    int K;
+// The control block of a chunk, in LDS.
+struct Ctl {
+    uint32_t n;         // candidate entries reserved
+    uint32_t tau_key;   // order key of the threshold (0: none yet)
+    uint32_t overflow;  // entries were dropped for want of room
+    uint32_t last;      // this work-group merges its row
+    float wave_t[16];   // per wave: its bound on the K-th quotient, and its largest quotient, of the first step
+    float wave_m[16];
+    uint32_t hist[kBuckets];  // appended quotients by bucket of the threshold histogram
 };
 
 // ------------------------------------------------------------------------------------------------------------------
-// Per-lane state of the streaming pass
+// Special tokens of a chunk, in LDS
 // ------------------------------------------------------------------------------------------------------------------
 
-struct Lane {
-    float bestx;    // greedy: this lane's largest final logit, and the first id holding it
-    int besti;
-    float lowq;     // the smallest quotient and the largest id holding it: the last token of the order
-    int lowi;
-    float mx, mn;   // largest and smallest final logits (NaN ignored)
-    double s;       // sum of exp(q - m) ...
-    float m;        // ... against m, the wave's running largest quotient (the same in every lane)
-    uint32_t flags; // kNaN, kTempOver, kNaN0, kBadHist
-};
-
-__device__ inline void lane_init(Lane & ln) {
-    ln.bestx = -INFINITY;
-    ln.besti = -1;
-    ln.lowq = INFINITY;
-    ln.lowi = -1;
-    ln.mx = -INFINITY;
-    ln.mn = INFINITY;
-    ln.s = 0.0;
-    ln.m = -FLT_MAX;
-    ln.flags = 0;
-}
-
-// ------------------------------------------------------------------------------------------------------------------
-// Special tokens of one chunk in LDS: for each 32 tokens a pair of words, the history bits and the banned bits, and
-// the number of history tokens before them, so a history token finds its slot in O(1)
-// ------------------------------------------------------------------------------------------------------------------
-
+// For each 32 tokens a word pair: .x the special bits (history of a penalized row, or banned), .y the history
+// vectors among the word's 16-byte vectors (low 8 bits) and the slot of the first of them (bits 8..31). A slot holds
+// one history vector: its index and history bits, the rank of its first history token among the chunk's (for the
+// counts), and the vector's raw 16 bytes, which the stream captures.
 struct Specials {
-    uint2 * bits;      // .x history, .y banned
-    int32_t * rank;    // history tokens before each word
-    int32_t * slot_id; // history ids of the chunk, rising
-    float * slot_raw;  // their raw logits, written by the stream
-    int32_t * slot_cnt;
+    uint2 * spec;
+    uint32_t * meta;    // per slot: (vector index << 8) | the vector's history bits
+    uint32_t * ufirst;  // per slot: rank of its first history token
+    uint32_t * cnt;     // per history token, by rank: its occurrences in the history
+    unsigned char * cap;
     int n_slots;
     bool any;
 };
 
-__device__ __forceinline__ int slot_of(const Specials & sp, int w, uint32_t hbits, int bit) {
-    return sp.rank[w] + __popc(hbits & ((1u << bit) - 1u));
+template <typename T>
+struct Elt;
+template <>
+struct Elt<float> {
+    static constexpr int V = 4;  // tokens per 16-byte vector
+    static constexpr int U = 4;  // vectors per lane per step
+};
+template <>
+struct Elt<uint16_t> {
+    static constexpr int V = 8;
+    static constexpr int U = 2;
+};
+
+// Bit v set where the v-th V-token vector of a word has a bit of h set.
+template <int V>
+__device__ inline uint32_t vec_mask(uint32_t h) {
+    uint32_t m = 0;
+#pragma unroll
+    for (int v = 0; v < 32 / V; v++) m |= ((h >> (v * V)) & ((1u << V) - 1u)) ? (1u << v) : 0u;
+    return m;
 }
 
-template <int B>
+template <int B, int V>
 __device__ inline void build_specials(Specials & sp, const Launch & a, int row, int c0, int c1, const Plan & pl,
                                       const uint32_t * banned_row, int * red, uint32_t & bad) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
-    for (int w = tid; w < nw; w += B) sp.bits[w] = make_uint2(0u, 0u);
+    for (int w = tid; w < nw; w += B) sp.spec[w] = make_uint2(0u, 0u);
     __syncthreads();
     int h0 = 0, h1 = 0;
     if (pl.pen) {
@@ -352,50 +335,539 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
             bad |= kBadHist;
             h1 = h0;
         }
+        // the history bits, in .y for now
         for (int j = h0 + tid; j < h1; j += B) {
             const int t = a.hist[j];
-            if (t >= c0 && t < c1) atomicOr(&sp.bits[(t - c0) >> 5].x, 1u << ((t - c0) & 31));
+            if (t >= c0 && t < c1) atomicOr(&sp.spec[(t - c0) >> 5].y, 1u << ((t - c0) & 31));
         }
+        __syncthreads();
     }
-    __syncthreads();
-    // Ranks and the slot list, each thread taking a run of words.
+    // Each thread takes a run of words: slots and history ranks by two scans, then the final word pairs.
     const int wpt = (nw + B - 1) / B;
     const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
-    int cnt = 0;
-    for (int w = w0; w < w1; w++) cnt += __popc(sp.bits[w].x);
-    int total;
-    int pos = block_excl_scan_i32<B>(cnt, red, total);
+    int nv = 0, nu = 0;
     for (int w = w0; w < w1; w++) {
-        sp.rank[w] = pos;
-        uint32_t b = sp.bits[w].x;
-        while (b) {
-            const int bit = __builtin_ctz(b);
-            b &= b - 1;
-            sp.slot_id[pos++] = c0 + (w << 5) + bit;
+        const uint32_t h = sp.spec[w].y;
+        nv += __popc(vec_mask<V>(h));
+        nu += __popc(h);
+    }
+    int tv, tu;
+    int vb = block_excl_scan_i32<B>(nv, red, tv);
+    int ub = block_excl_scan_i32<B>(nu, red, tu);
+    for (int w = w0; w < w1; w++) {
+        const uint32_t h = sp.spec[w].y;
+        const uint32_t occ = vec_mask<V>(h);
+        uint32_t bw = 0;
+        if (banned_row) {
+            bw = banned_row[(c0 >> 5) + w];
+            const int base = c0 + (w << 5);
+            if (base + 32 > c1) bw &= (1u << (c1 - base)) - 1u;  // 0 < c1 - base < 32 here
+        }
+        sp.spec[w] = make_uint2(h | bw, ((uint32_t) vb << 8) | occ);
+        uint32_t o = occ;
+        while (o) {
+            const int v = __builtin_ctz(o);
+            o &= o - 1;
+            const uint32_t hm = (h >> (v * V)) & ((1u << V) - 1u);
+            sp.meta[vb] = ((uint32_t) (w * (32 / V) + v) << 8) | hm;
+            sp.ufirst[vb] = (uint32_t) ub;
+            ub += __popc(hm);
+            vb++;
         }
     }
-    sp.n_slots = total;
+    sp.n_slots = tv;
     __syncthreads();
     if (pl.counts) {
-        for (int s = tid; s < total; s += B) sp.slot_cnt[s] = 0;
+        for (int s = tid; s < tu; s += B) sp.cnt[s] = 0;
         __syncthreads();
         for (int j = h0 + tid; j < h1; j += B) {
             const int t = a.hist[j];
             if (t >= c0 && t < c1) {
                 const int o = t - c0;
-                atomicAdd(&sp.slot_cnt[slot_of(sp, o >> 5, sp.bits[o >> 5].x, o & 31)], 1);
+                const uint32_t info = sp.spec[o >> 5].y;
+                const int vpos = (o & 31) / V;
+                const int slot = (int) (info >> 8) + __popc(info & ((1u << vpos) - 1u) & 0xffu);
+                const int jj = o & (V - 1);
+                const uint32_t hm = sp.meta[slot] & 0xffu;
+                atomicAdd(&sp.cnt[sp.ufirst[slot] + __popc(hm & ((1u << jj) - 1u))], 1u);
+            }
+        }
+        __syncthreads();
+    }
+}
+
+template <typename T>
+__device__ inline float load_one(const T * p);
+template <>
+__device__ inline float load_one<float>(const float * p) {
+    return *p;
+}
+template <>
+__device__ inline float load_one<uint16_t>(const uint16_t * p) {
+    return bf16_to_float(*p);
+}
+
+template <typename T>
+__device__ inline float cap_value(const unsigned char * slot, int j);
+template <>
+__device__ inline float cap_value<float>(const unsigned char * slot, int j) {
+    return ((const float *) slot)[j];
+}
+template <>
+__device__ inline float cap_value<uint16_t>(const unsigned char * slot, int j) {
+    return bf16_to_float(((const uint16_t *) slot)[j]);
+}
+
+// A history token of the chunk by its (slot, position) index: its id and final logit (penalized; -inf when banned).
+struct HistTok {
+    int id;
+    float v;
+    bool banned;
+};
+
+template <typename T, int V>
+__device__ inline bool hist_token(const Specials & sp, int i, int c0, const spx_row_params & p, const Plan & pl,
+                                  const uint32_t * banned_row, const T * rowp, bool captured, HistTok & h) {
+    const int s = i / V, j = i & (V - 1);
+    const uint32_t meta = sp.meta[s];
+    if (!((meta >> j) & 1u)) return false;
+    h.id = c0 + (int) (meta >> 8) * V + j;
+    const float raw = captured ? cap_value<T>(sp.cap + (size_t) s * 16, j) : load_one<T>(rowp + h.id);
+    const int c = pl.counts ? (int) sp.cnt[sp.ufirst[s] + __popc(meta & ((1u << j) - 1u) & 0xffu)] : 1;
+    float v = penalize(raw, c, p);
+    h.banned = banned_row && ((banned_row[h.id >> 5] >> (h.id & 31)) & 1u);
+    if (h.banned) v = -INFINITY;
+    h.v = v;
+    return true;
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The stream: sampling rows
+// ------------------------------------------------------------------------------------------------------------------
+
+struct SampleSt {
+    double s;        // lane: sum of 2^(q*L - hi) over its groups, L = log2(e) in float
+    float m, hi;     // wave: the reference quotient and RN(m*L) (-FLT_MAX while no finite quotient is known)
+    float tau;       // wave: a quotient at or above it enters the buffer
+    float lo, inv, delta;  // wave: the bucket map of the histogram, bucket b = (q - lo) * inv
+    int hist_on;
+    uint32_t flags;  // lane
+};
+
+// The first step: every wave bounds the K-th quotient by the kw-th largest of its lanes' maxima (each lane's maximum
+// is a distinct token), the work-group takes the smallest bound (kw lanes of every wave lie at or above it: at least
+// K tokens) and the largest quotient as the reference m.
+template <int B>
+__device__ __forceinline__ void bootstrap(const Plan & pl, SampleSt & st, Ctl * ctl, const float (&q)[kE]) {
+    constexpr int W = B / kWave;
+    float lm = -INFINITY;
+#pragma unroll
+    for (int k = 0; k < kE; k++) lm = fmaxf(lm, q[k] < INFINITY ? q[k] : -INFINITY);
+    const float wmax = wave_max_f32(lm);
+    const int kw = (pl.K + W - 1) / W;
+    float v = lm, kth = -INFINITY;
+    for (int r = 0; r < kw; r++) {
+        const float mx = uniform_f(wave_max_f32(v));
+        kth = mx;
+        if (!(mx > -INFINITY)) break;
+        const uint64_t eq = ballot(v == mx);
+        if (lane_id() == (int) __builtin_ctzll(eq)) v = -INFINITY;
+    }
+    const int wave = threadIdx.x / kWave;
+    if (lane_id() == 0) {
+        ctl->wave_t[wave] = kth;
+        ctl->wave_m[wave] = wmax;
+    }
+    __syncthreads();
+    float tau0 = INFINITY, mref = -INFINITY;
+    for (int w = 0; w < W; w++) {
+        tau0 = fminf(tau0, ctl->wave_t[w]);
+        mref = fmaxf(mref, ctl->wave_m[w]);
+    }
+    tau0 = uniform_f(tau0);
+    mref = uniform_f(mref);
+    st.tau = tau0;
+    st.m = mref;
+    st.hi = mref > -INFINITY ? mref * kL2e : -FLT_MAX;
+    const float span = mref - tau0;
+    st.hist_on = (tau0 > -INFINITY && span > 0.0f && span < INFINITY) ? 1 : 0;
+    st.lo = tau0;
+    st.inv = st.hist_on ? 120.0f / span : 0.0f;
+    st.delta = st.hist_on ? span / 120.0f : 0.0f;
+    if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tau0));
+}
+
+// A group with a term that is not a finite number below 2^100: exact quotients, the flags, a new reference m where a
+// finite quotient passes the old one, and the group's sum again.
+__device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE], const float (&x)[kE], uint32_t kill,
+                                  bool mask) {
+    float gm = -INFINITY;
+    uint32_t fl = 0;
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        float qe = -INFINITY;
+        if (!(mask && ((kill >> k) & 1u))) {
+            const float xv = x[k];
+            qe = div_rn(xv, pl.t, pl.rt);
+            if (__builtin_isnan(qe)) fl |= kNaN;
+            else if (qe == INFINITY) fl |= xv == INFINITY ? kPosInf : kTempOver;
+            else if (qe == -INFINITY) fl |= xv == -INFINITY ? kNegInf : kTempOver;
+            else gm = fmaxf(gm, qe);
+            if (__builtin_isfinite(xv)) fl |= kFinite;
+        }
+        q[k] = qe;
+    }
+    st.flags |= fl;
+    const float wm = uniform_f(wave_max_f32(gm));
+    if (wm > st.m) {
+        const float nhi = wm * kL2e;
+        if (st.m > -INFINITY) st.s *= exp2((double) st.hi - (double) nhi);
+        st.m = wm;
+        st.hi = nhi;
+    }
+    float acc = 0.0f;
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        const float qv = q[k];
+        if (qv > -INFINITY && qv < INFINITY) acc += __builtin_amdgcn_exp2f(__builtin_fmaf(qv, kL2e, -st.hi));
+    }
+    st.s += (double) acc;
+}
+
+// A bound on the K-th appended quotient from the histogram: the boundary of the highest bucket with at least K
+// appended quotients at or above it, less one bucket (the float rounding of (q - lo) * inv cannot move a counted
+// quotient under it); -inf when there is none.
+__device__ __forceinline__ float hist_bound(const uint32_t * hist, int K, float lo, float delta) {
+    const int l = lane_id();
+    const uint32_t ha = hist[kBuckets - 1 - 2 * l], hb = hist[kBuckets - 2 - 2 * l];
+    const int incl = wave_incl_scan_i32((int) (ha + hb));  // appended at or above bucket kBuckets-2-2l
+    const uint64_t ge = ballot(incl >= K);
+    if (!ge) return -INFINITY;
+    const int l0 = (int) __builtin_ctzll(ge);
+    const int in0 = __builtin_amdgcn_readlane(incl, l0), hb0 = __builtin_amdgcn_readlane((int) hb, l0);
+    const int bstar = (in0 - hb0 >= K) ? kBuckets - 1 - 2 * l0 : kBuckets - 2 - 2 * l0;
+    if (bstar < 2) return -INFINITY;
+    return lo + (float) (bstar - 1) * delta;
+}
+
+// The K-th largest key among the first `lim` entries of the buffer (entries other waves have reserved but not
+// written yet read as 0 and are not counted); 0 when there are fewer than K. Taken when the buffer fills past a half
+// and three quarters, which happens where the histogram has no range (no bound from the first step) or the logits
+// come in rising order.
+__device__ __forceinline__ uint32_t buffer_bound(const uint64_t * cand, int lim, int K) {
+    constexpr int kMaxPerLane = 24;  // lim <= 3/4 of a buffer of 2048 entries
+    const int l = lane_id();
+    uint32_t keys[kMaxPerLane];
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; j++) {
+        const int i = l + kWave * j;
+        keys[j] = i < lim ? (uint32_t) (cand[i] >> 32) : 0u;
+    }
+    uint32_t key = 0;
+    for (int b = 31; b >= 0; b--) {
+        const uint32_t c = key | (1u << b);
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; j++) cnt += keys[j] >= c ? 1 : 0;
+        if (wave_sum_i32(cnt) >= K) key = c;
+    }
+    return key;
+}
+
+// Appends the lanes' passing quotients to the buffer: each lane writes its own run, placed by a scan over the wave;
+// one atomic per wave reserves the room. `all` (no bound yet) takes every valid element, -inf ones included.
+template <int B, int VV, bool MASK>
+__device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
+                                            const float (&q)[kE], const float (&x)[kE], uint32_t kill, int id_base) {
+    const bool all = !(st.tau > -INFINITY);
+    uint32_t pass = 0;
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        const bool live = !MASK || !((kill >> k) & 1u);
+        const bool p = all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau);
+        pass |= p ? (1u << k) : 0u;
+    }
+    const int c = __popc(pass);
+    const int incl = wave_incl_scan_i32(c);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    uint32_t base = 0;
+    if (lane_id() == 0) base = atomicAdd(&ctl->n, (uint32_t) total);
+    base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
+    if (base + (uint32_t) total > (uint32_t) cap && lane_id() == 0) ctl->overflow = 1u;
+    int pos = (int) base + incl - c;
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        if ((pass >> k) & 1u) {
+            if (pos < cap) {
+                // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
+                float qq = q[k];
+                if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = x[k] / pl.t;
+                const int id = id_base + (k / VV) * (B * VV) + (k % VV);
+                cand[pos] = make_entry(order_key(qq), (uint32_t) id);
+                if (st.hist_on) {
+                    const float bf = fminf((qq - st.lo) * st.inv, (float) (kBuckets - 1));
+                    atomicAdd(&ctl->hist[max((int) bf, 0)], 1u);
+                }
+            }
+            pos++;
+        }
+    }
+    const uint32_t end = base + (uint32_t) total;
+    const uint32_t l1 = (uint32_t) cap / 2, l2 = (uint32_t) cap / 4 * 3;
+    float tn = -INFINITY;
+    if ((base < l1 && end >= l1) || (base < l2 && end >= l2)) {
+        const uint32_t kk = buffer_bound(cand, (int) (base < l1 ? l1 : l2), pl.K);
+        if (kk) tn = key_float(kk);
+    } else if (st.hist_on) {
+        tn = hist_bound(ctl->hist, pl.K, st.lo, st.delta);
+    }
+    tn = uniform_f(tn);
+    if (tn > st.tau) {
+        st.tau = tn;
+        if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tn));
+    }
+}
+
+// One group of kE final logits per lane. x: raw logits; kill: elements that are special tokens or out of range;
+// rdead: those out of range. Element k's token is id_base + (k / VV) * B * VV + k % VV.
+template <int B, int VV, bool MASK, bool BOOT>
+__device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
+                                            const float (&x)[kE], uint32_t kill, uint32_t rdead, int id_base) {
+    float q[kE];
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        // x / t correctly rounded for a quotient in the normal range (Markstein's correction step)
+        const float q0 = x[k] * pl.rt;
+        q[k] = __builtin_fmaf(__builtin_fmaf(-q0, pl.t, x[k]), pl.rt, q0);
+    }
+    if (MASK) {
+#pragma unroll
+        for (int k = 0; k < kE; k++) q[k] = kill_to(q[k], kill, k);
+    }
+    if (BOOT) bootstrap<B>(pl, st, ctl, q);
+    float t[kE];
+#pragma unroll
+    for (int k = 0; k < kE; k++) t[k] = __builtin_amdgcn_exp2f(__builtin_fmaf(q[k], kL2e, -st.hi));
+#pragma unroll
+    for (int w = kE / 2; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int k = 0; k < w; k++) t[k] += t[k + w];
+    }
+    if (ballot(!(t[0] <= 0x1p100f))) slow_group(pl, st, q, x, kill, MASK);
+    else st.s += (double) t[0];
+    // Candidates: the lane's largest quotient against tau first (NaN never passes), the lanes' runs only then.
+    bool any;
+    if (st.tau > -INFINITY) {
+        float tq[kE];
+#pragma unroll
+        for (int k = 0; k < kE; k++) tq[k] = q[k];
+#pragma unroll
+        for (int w = kE / 2; w >= 1; w >>= 1) {
+#pragma unroll
+            for (int k = 0; k < w; k++) tq[k] = fmaxf(tq[k], tq[k + w]);
+        }
+        any = ballot(tq[0] >= st.tau) != 0;
+    } else {
+        any = true;
+    }
+    if (any) insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base);
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The stream: greedy rows
+// ------------------------------------------------------------------------------------------------------------------
+
+struct GreedySt {
+    float bx;       // lane: its largest final logit and the first token holding it (tokens come in rising order)
+    int bi;
+    float xmin;     // lane: smallest raw logit in range
+    uint64_t nanb;  // wave: lanes that met a NaN final logit
+};
+
+template <int B, int VV, bool MASK>
+__device__ __forceinline__ void greedy_core(const Plan & pl, GreedySt & g, const float (&x)[kE], uint32_t kill,
+                                            uint32_t rdead, int id_base) {
+    float xm[kE];
+#pragma unroll
+    for (int k = 0; k < kE; k++) xm[k] = MASK ? kill_to(x[k], kill, k) : x[k];
+    if (pl.nanchk) {
+#pragma unroll
+        for (int k = 0; k < kE; k++) g.nanb |= ballot(xm[k] != xm[k]);
+    }
+    if (pl.xmin) {
+#pragma unroll
+        for (int k = 0; k < kE; k++) g.xmin = fminf(g.xmin, ((rdead >> k) & 1u) ? INFINITY : x[k]);
+    }
+    float t[kE];
+#pragma unroll
+    for (int k = 0; k < kE; k++) t[k] = xm[k];
+#pragma unroll
+    for (int w = kE / 2; w >= 1; w >>= 1) {
+#pragma unroll
+        for (int k = 0; k < w; k++) t[k] = fmaxf(t[k], t[k + w]);
+    }
+    const float gx = t[0];
+    if (ballot(gx > g.bx)) {
+        if (gx > g.bx) {
+            int idx = 0;
+#pragma unroll
+            for (int k = kE - 1; k >= 0; k--) idx = xm[k] == gx ? k : idx;
+            g.bx = gx;
+            g.bi = id_base + (idx / VV) * (B * VV) + (idx % VV);
+        }
+    }
+}
+
+// ------------------------------------------------------------------------------------------------------------------
+// The stream over a chunk
+// ------------------------------------------------------------------------------------------------------------------
+
+using U32x4 = uint32_t __attribute__((ext_vector_type(4)));
+
+template <typename T>
+__device__ inline void unpack(const U32x4 & r, float * x);
+template <>
+__device__ inline void unpack<float>(const U32x4 & r, float * x) {
+    x[0] = __uint_as_float(r.x);
+    x[1] = __uint_as_float(r.y);
+    x[2] = __uint_as_float(r.z);
+    x[3] = __uint_as_float(r.w);
+}
+template <>
+__device__ inline void unpack<uint16_t>(const U32x4 & r, float * x) {
+    x[0] = __uint_as_float(r.x << 16);
+    x[1] = __uint_as_float(r.x & 0xffff0000u);
+    x[2] = __uint_as_float(r.y << 16);
+    x[3] = __uint_as_float(r.y & 0xffff0000u);
+    x[4] = __uint_as_float(r.z << 16);
+    x[5] = __uint_as_float(r.z & 0xffff0000u);
+    x[6] = __uint_as_float(r.w << 16);
+    x[7] = __uint_as_float(r.w & 0xffff0000u);
+}
+
+struct StreamCtx {
+    const Plan * pl;
+    const Specials * sp;
+    bool cap_on;     // capture history vectors
+    SampleSt * st;
+    GreedySt * g;
+    Ctl * ctl;
+    uint64_t * cand;
+    int cap;
+};
+
+template <int B, int VV, bool MASK, bool BOOT, bool GREEDY>
+__device__ __forceinline__ void run_core(StreamCtx & c, const float (&x)[kE], uint32_t kill, uint32_t rdead, int id_base) {
+    if constexpr (GREEDY) greedy_core<B, VV, MASK>(*c.pl, *c.g, x, kill, rdead, id_base);
+    else sample_core<B, VV, MASK, BOOT>(*c.pl, *c.st, c.ctl, c.cand, c.cap, x, kill, rdead, id_base);
+}
+
+// kE tokens per lane, one each at chunk offsets o0 + k*B: rows that are not 16-byte aligned, and a chunk's tail.
+template <typename T, int B, bool SPEC, bool GREEDY, bool BOOT>
+__device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int c0, int n, int o0) {
+    constexpr int V = Elt<T>::V;
+    float x[kE];
+    uint32_t kill = 0, rdead = 0;
+#pragma unroll
+    for (int k = 0; k < kE; k++) {
+        const int o = o0 + k * B;
+        x[k] = 0.0f;
+        if (o < n) {
+            const T raw = rowp[c0 + o];
+            x[k] = load_one<T>(&raw);
+            if (SPEC) {
+                const uint2 pr = c.sp->spec[o >> 5];
+                if ((pr.x >> (o & 31)) & 1u) {
+                    kill |= 1u << k;
+                    const int vpos = (o & 31) / V;
+                    if (c.cap_on && ((pr.y >> vpos) & 1u)) {
+                        const int slot = (int) (pr.y >> 8) + __popc(pr.y & ((1u << vpos) - 1u));
+                        ((T *) (c.sp->cap + (size_t) slot * 16))[o & (V - 1)] = raw;
+                    }
+                }
+            }
+        } else {
+            rdead |= 1u << k;
+        }
+    }
+    run_core<B, 1, true, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + o0);
+}
+
+// One step of the vector stream: U vectors per lane, vector g0 + u*B for u < U, of which those past the last whole
+// vector (ng) are out of range when RANGE. Captures the history vectors; BOOT is the first step.
+template <typename T, int B, bool SPEC, bool GREEDY, bool RANGE, bool BOOT>
+__device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T>::U], int c0, int g0, int ng, int gl,
+                                         bool cap_vec) {
+    constexpr int V = Elt<T>::V, U = Elt<T>::U, VW = 32 / V;
+    constexpr uint32_t VM = (1u << V) - 1u;
+    float x[kE];
+#pragma unroll
+    for (int u = 0; u < U; u++) unpack<T>(cur[u], x + u * V);
+    uint32_t kill = 0;
+    if (SPEC) {
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int gg = RANGE ? min(g0 + u * B, gl) : g0 + u * B;
+            const uint2 pr = c.sp->spec[gg / VW];
+            const int vpos = gg & (VW - 1);
+            kill |= ((pr.x >> (vpos * V)) & VM) << (u * V);
+            if (cap_vec && ((pr.y >> vpos) & 1u)) {
+                const int slot = (int) (pr.y >> 8) + __popc(pr.y & ((1u << vpos) - 1u));
+                *(U32x4 *) (c.sp->cap + (size_t) slot * 16) = cur[u];
             }
         }
     }
-    if (banned_row) {
-        for (int w = tid; w < nw; w += B) {
-            uint32_t bw = banned_row[(c0 >> 5) + w];
-            const int base = c0 + (w << 5);
-            if (base + 32 > c1) bw &= (1u << (c1 - base)) - 1u;  // 0 < c1 - base < 32 here
-            sp.bits[w].y = bw;
-        }
+    uint32_t rdead = 0;
+    if (RANGE) {
+#pragma unroll
+        for (int u = 0; u < U; u++) rdead |= (g0 + u * B < ng) ? 0u : (VM << (u * V));
     }
-    __syncthreads();
+    run_core<B, V, SPEC || RANGE, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + g0 * V);
+}
+
+template <typename T, int B, bool SPEC, bool GREEDY>
+__device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * rowp, int c0, int c1) {
+    constexpr int V = Elt<T>::V, U = Elt<T>::U;
+    const int n = c1 - c0, tid = threadIdx.x;
+    if (!a.vec_ok) {
+        const int nit = max(1, (n + kE * B - 1) / (kE * B));
+        scalar_group<T, B, SPEC, GREEDY, true>(c, rowp, c0, n, tid);
+        for (int it = 1; it < nit; it++) scalar_group<T, B, SPEC, GREEDY, false>(c, rowp, c0, n, it * kE * B + tid);
+        return;
+    }
+    const int ng = n / V;  // whole vectors
+    constexpr int per = U * B;
+    const int nit = ng > 0 ? (ng + per - 1) / per : 1;
+    const int gl = max(ng - 1, 0);
+    const U32x4 * vp = (const U32x4 *) (rowp + c0);
+    const bool cap_vec = c.cap_on && ng > 0;
+    // The first and last steps (lanes past the last vector load it again and take nothing from it) are peeled off
+    // the steady loop, whose loads for the next step are in flight while a step is worked on.
+    U32x4 cur[U], nxt[U];
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+        cur[u] = U32x4{0u, 0u, 0u, 0u};
+        nxt[u] = cur[u];
+    }
+    if (ng > 0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) cur[u] = vp[min(tid + u * B, gl)];
+    }
+    if (nit > 1) {
+#pragma unroll
+        for (int u = 0; u < U; u++) nxt[u] = vp[min(per + tid + u * B, gl)];
+    }
+    vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl, cap_vec);
+    for (int it = 1; it + 1 < nit; it++) {
+#pragma unroll
+        for (int u = 0; u < U; u++) cur[u] = nxt[u];
+        const int g0 = it * per + tid;
+#pragma unroll
+        for (int u = 0; u < U; u++) nxt[u] = vp[min(g0 + per + u * B, gl)];
+        vec_step<T, B, SPEC, GREEDY, false, false>(c, cur, c0, g0, ng, gl, cap_vec);
+    }
+    if (nit > 1) vec_step<T, B, SPEC, GREEDY, true, false>(c, nxt, c0, (nit - 1) * per + tid, ng, gl, cap_vec);
+    if (n - ng * V > 0) scalar_group<T, B, SPEC, GREEDY, false>(c, rowp, c0, n, ng * V + tid);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -403,25 +875,23 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
 // ------------------------------------------------------------------------------------------------------------------
 
 struct RowTotals {
-    uint64_t best;  // greedy: make_entry(key, id) of the first largest final logit (0: none above -inf)
-    uint64_t low;   // (key << 32 | ~id) of the last token of the order (all ones: none)
-    double s;       // sum of exp(q - m) ...
-    float m;        // ... relative to m
-    float mx, mn;
+    uint64_t best;   // greedy: the largest entry of the final logits (0: none above -inf)
+    double s;        // sum of exp(q - m) over the row
+    float m;
     uint32_t flags;
 };
 
 // The row status, as the reference's checks order them; -1 when the row goes on.
-__device__ inline int row_status(const Plan & pl, const spx_row_params & p, const RowTotals & t, bool top_finite) {
-    const uint32_t f = t.flags;
+__device__ inline int row_status(const Plan & pl, const spx_row_params & p, uint32_t f, bool top_finite) {
     if (pl.mode == kInvalid || (f & kBadHist)) return SPX_ROW_INVALID_PARAMS;
     const bool pen = !neutral(p);
-    const bool posinf = t.mx == INFINITY;
+    const bool posinf = (f & kPosInf) != 0;
+    const bool anyf = (f & (kFinite | kPosInf)) != 0;  // the largest final logit is above -inf
     if (pl.flavor == SPX_FLAVOR_TRANSFORMERS) {
         // restricted(): std::max_element's largest, a NaN in front taken as it (src/families/qwen3-tts/sampler.cpp:43-49)
         if (f & kNaN0) return SPX_ROW_NO_FINITE_LOGIT;
         if (posinf) return pen ? SPX_ROW_REP_PENALTY_OVERFLOW : SPX_ROW_NO_FINITE_LOGIT;
-        if (!(t.mx > -INFINITY)) return SPX_ROW_NO_FINITE_LOGIT;
+        if (!anyf) return SPX_ROW_NO_FINITE_LOGIT;
         if (pl.mode == kGreedy) return -1;
         if (f & kNaN) return SPX_ROW_NONFINITE_INPUT;
         if (!top_finite) return SPX_ROW_TEMPERATURE_OVERFLOW;  // qwen3-tts/sampler.cpp:82-83
@@ -434,7 +904,7 @@ __device__ inline int row_status(const Plan & pl, const spx_row_params & p, cons
         if (f & kTempOver) return SPX_ROW_TEMPERATURE_OVERFLOW;  // haru/sampler.cpp:33-35
         return -1;
     }
-    if ((f & kNaN) || posinf || t.mn == -INFINITY) return SPX_ROW_NONFINITE_INPUT;  // drama3/sampler.cpp:35-37
+    if ((f & kNaN) || posinf || (f & kNegInf)) return SPX_ROW_NONFINITE_INPUT;  // drama3/sampler.cpp:35-37
     if (pl.mode == kGreedy) return -1;
     if (!top_finite) return SPX_ROW_TEMPERATURE_OVERFLOW;  // drama3/sampler.cpp:46-47
     return -1;
@@ -446,23 +916,32 @@ __device__ inline void write_row(const Launch & a, int row, int id, int status, 
     if (a.out_kept) a.out_kept[row] = status == SPX_ROW_OK ? kept : 0;
 }
 
+// The flags a greedy row's largest entry settles.
+__device__ inline uint32_t best_flags(uint64_t best) {
+    if (!best) return 0u;
+    const float v = entry_value(best);
+    return v == INFINITY ? kPosInf : (v > -INFINITY ? kFinite : 0u);
+}
+
 // Scratch of the finishing step, in LDS.
 struct FinishLds {
-    double * w;     // weights, kKeep
-    double * red;   // reduction scratch
+    double * w;   // weights, up to B
+    double * red;
     int * ired;
-    float * pf;     // float weights (HARU), kKeep
+    float * pf;   // float weights (HARU), up to B
 };
 
-// Finishes a row from its totals and its n sorted top entries e[0..n). Returns true when the row is done, false when
-// it needs the multi-pass path (its top-p set or its draw runs beyond the entries kept).
+constexpr int kNone = 0x7fffffff;
+
+// Finishes a row from its totals and its n sorted top entries e[0..n), n <= B. Returns true when the row is done,
+// false when it needs the multi-pass path (its top-p set or its draw runs beyond the entries held).
 template <int B>
 __device__ inline bool finish_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
                                   const RowTotals & tot, const uint64_t * e, int n, bool complete, FinishLds & L) {
     const int tid = threadIdx.x;
     const double u = a.u ? a.u[row] : 0.0;
     const float top = n > 0 ? entry_value(e[0]) : -INFINITY;
-    const int st = row_status(pl, p, tot, n > 0 && __builtin_isfinite(top));
+    const int st = row_status(pl, p, tot.flags, n > 0 && __builtin_isfinite(top));
     if (st >= 0) {
         if (tid == 0) write_row(a, row, -1, st, 0);
         return true;
@@ -485,9 +964,11 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
     // Every candidate of the reference with a weight is held: its top k, or every token that has a key (the rest of
     // a short row are banned tokens, last in the order with weight 0).
     const bool full_known = nk >= pl.k || complete;
+    // the k-th candidate itself is held (it is not a banned token beyond the entries)
+    const bool last_held = nk >= pl.k;
     const bool valid = tid < nk;
     const float vi = valid ? entry_value(e[tid]) : -INFINITY;
-    // The sum of exp over the whole vocabulary, relative to the top value (the m of the totals is that value).
+    // The sum of exp over the whole vocabulary, relative to the top value (m of the totals is that value or below).
     const double s_all = pl.need_s ? tot.s * exp((double) tot.m - (double) top) : 0.0;
     int kept = 0, pick = -1;
     bool resolved = true;
@@ -504,8 +985,8 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
         if (pl.top_p < 1.0f) {
             // the smallest prefix whose cumulative weight reaches top_p, at least one (:88-99)
             const double c = block_incl_scan_f64<B>(q, L.red);
-            const int first = block_min_i32<B>(valid && c >= (double) pl.top_p ? tid : 0x7fffffff, L.ired);
-            if (first != 0x7fffffff) keep = first + 1;
+            const int first = block_min_i32<B>(valid && c >= (double) pl.top_p ? tid : kNone, L.ired);
+            if (first != kNone) keep = first + 1;
             else if (full_known) keep = nk;
             else resolved = false;
         } else if (full_known) {
@@ -514,8 +995,8 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
             // A draw over every token: pick()'s running share must pass u within the entries held. The shares are
             // the weights over the whole vocabulary's sum, which is what pick() divides by, to rounding.
             const double c = block_incl_scan_f64<B>(q, L.red);
-            const int first = block_min_i32<B>(valid && c > u ? tid : 0x7fffffff, L.ired);
-            if (first != 0x7fffffff && first < pl.k - 1) {
+            const int first = block_min_i32<B>(valid && c > u ? tid : kNone, L.ired);
+            if (first != kNone && first < pl.k - 1) {
                 pick = first;
                 kept = pl.k;
                 if (a.out_cand_ids && valid && tid < a.max_out) {
@@ -527,14 +1008,19 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
             }
         }
         if (keep > 0) {
-            // pick() over the kept weights (src/common/sampling.cpp:9-19)
+            // pick() over the kept weights (src/common/sampling.cpp:9-19). Where every token is held but fewer than
+            // k have a key (banned ones, weight 0, are the rest of the k), the last held is not pick()'s last.
+            const bool short_k = pl.top_p >= 1.0f && !last_held;
+            const int lim = short_k ? keep : keep - 1;
             const bool in = tid < keep;
             const double kq = in ? q : 0.0;
             const double ksum = block_sum_f64<B>(kq, L.red);
             const double c = block_incl_scan_f64<B>(in ? kq / ksum : 0.0, L.red);
-            const int first = block_min_i32<B>(in && tid < keep - 1 && c > u ? tid : 0x7fffffff, L.ired);
-            pick = first != 0x7fffffff ? first : keep - 1;
-            kept = keep;
+            const int first = block_min_i32<B>(in && tid < lim && c > u ? tid : kNone, L.ired);
+            if (first != kNone) pick = first;
+            else if (!short_k) pick = keep - 1;
+            else resolved = false;
+            kept = short_k ? pl.k : keep;
             if (a.out_cand_ids && in && tid < a.max_out) {
                 a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
                 a.out_cand_probs[(int64_t) row * a.max_out + tid] = (float) (kq / ksum);
@@ -570,24 +1056,25 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
                     L.w[i] = zero ? 0.0 : (double) pi;
                     zeros += zero ? 1 : 0;
                 }
-                L.ired[8] = zeros;
+                L.ired[48] = zeros;
             }
         } else if (tid == 0) {
             for (int i = 0; i < nk; i++) L.w[i] = (double) L.pf[i];
-            L.ired[8] = 0;
+            L.ired[48] = 0;
         }
         __syncthreads();
         // Beyond the entries held the weights must be 0: a zero among them, the cumulative share only rising.
-        if (!full_known && L.ired[8] == 0) resolved = false;
+        if (!full_known && L.ired[48] == 0) resolved = false;
         const double w = valid ? L.w[tid] : 0.0;
         __syncthreads();
         if (resolved) {
+            // pick() over all k weights, zeros included: the held k-th is its last; short of it, its last lies beyond
+            const int lim = last_held ? nk - 1 : nk;
             const double ksum = block_sum_f64<B>(w, L.red);
             const double c = block_incl_scan_f64<B>(w / ksum, L.red);
-            const int first = block_min_i32<B>(valid && tid < nk - 1 && c > u ? tid : 0x7fffffff, L.ired);
-            if (first != 0x7fffffff) pick = first;
-            else if (full_known) pick = nk - 1;  // pick()'s last, which may weigh 0
-            else if (pl.need_low) pick = -2;     // the last token of the whole order
+            const int first = block_min_i32<B>(valid && tid < lim && c > u ? tid : kNone, L.ired);
+            if (first != kNone) pick = first;
+            else if (last_held) pick = nk - 1;
             else resolved = false;
             kept = pl.k;
             if (a.out_cand_ids && valid && tid < a.max_out) {
@@ -600,9 +1087,9 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
         // (src/families/drama3/sampler.cpp:48-59)
         const double w = valid ? exp((double) vi - (double) top) : 0.0;
         const double c = block_incl_scan_f64<B>(w / s_all, L.red);
-        const int first = block_min_i32<B>(valid && tid > 0 && c > (double) pl.top_p ? tid : 0x7fffffff, L.ired);
+        const int first = block_min_i32<B>(valid && tid > 0 && c > (double) pl.top_p ? tid : kNone, L.ired);
         int keep;
-        if (first != 0x7fffffff) keep = first;
+        if (first != kNone) keep = first;
         else if (full_known) keep = nk;
         else {
             keep = -1;
@@ -613,8 +1100,8 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
             const double kw = in ? w : 0.0;
             const double ksum = block_sum_f64<B>(kw, L.red);
             const double cc = block_incl_scan_f64<B>(kw / ksum, L.red);
-            const int f2 = block_min_i32<B>(in && tid < keep - 1 && cc > u ? tid : 0x7fffffff, L.ired);
-            pick = f2 != 0x7fffffff ? f2 : keep - 1;
+            const int f2 = block_min_i32<B>(in && tid < keep - 1 && cc > u ? tid : kNone, L.ired);
+            pick = f2 != kNone ? f2 : keep - 1;
             kept = keep;
             if (a.out_cand_ids && in && tid < a.max_out) {
                 a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
@@ -623,10 +1110,7 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
         }
     }
     if (!resolved) return false;
-    if (tid == 0) {
-        const int id = pick == -2 ? (int) ~(uint32_t) tot.low : (int) entry_id(e[pick]);
-        write_row(a, row, id, SPX_ROW_OK, kept);
-    }
+    if (tid == 0) write_row(a, row, (int) entry_id(e[pick]), SPX_ROW_OK, kept);
     if (a.out_cand_ids) {
         // entries past those written above
         for (int j = min(kept, nk) + tid; j < a.max_out; j += B) {
@@ -638,365 +1122,6 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
 }
 
 // ------------------------------------------------------------------------------------------------------------------
-// The streaming pass
-// ------------------------------------------------------------------------------------------------------------------
-
-template <typename T>
-__device__ inline float load_one(const T * p);
-template <>
-__device__ inline float load_one<float>(const float * p) {
-    return *p;
-}
-template <>
-__device__ inline float load_one<uint16_t>(const uint16_t * p) {
-    return bf16_to_float(*p);
-}
-
-using U32x4 = uint32_t __attribute__((ext_vector_type(4)));
-
-template <typename T>
-struct Vec;
-template <>
-struct Vec<float> {
-    static constexpr int n = 4;
-    __device__ static inline void unpack(const U32x4 & r, float (&x)[4]) {
-        x[0] = __uint_as_float(r.x);
-        x[1] = __uint_as_float(r.y);
-        x[2] = __uint_as_float(r.z);
-        x[3] = __uint_as_float(r.w);
-    }
-};
-template <>
-struct Vec<uint16_t> {
-    static constexpr int n = 8;
-    __device__ static inline void unpack(const U32x4 & r, float (&x)[8]) {
-        x[0] = __uint_as_float(r.x << 16);
-        x[1] = __uint_as_float(r.x & 0xffff0000u);
-        x[2] = __uint_as_float(r.y << 16);
-        x[3] = __uint_as_float(r.y & 0xffff0000u);
-        x[4] = __uint_as_float(r.z << 16);
-        x[5] = __uint_as_float(r.z & 0xffff0000u);
-        x[6] = __uint_as_float(r.w << 16);
-        x[7] = __uint_as_float(r.w & 0xffff0000u);
-    }
-};
-
-// The wave's candidate offers of one vector: lanes of `ok` whose quotient reaches tf enter the buffer, after a
-// compaction where the buffer would overflow (which raises tf to the wave's new K-th key).
-template <int V>
-__device__ __forceinline__ void offer_vec(WaveBuf & wb, uint32_t * wg_tau, const float (&q)[V], uint32_t ok, float & tf,
-                                          int i0) {
-    uint64_t m[V];
-    int cnt = 0;
-#pragma unroll
-    for (int j = 0; j < V; j++) {
-        m[j] = ballot(((ok >> j) & 1u) && q[j] >= tf);
-        cnt += (int) __popcll(m[j]);
-    }
-    if (cnt == 0) return;
-    if (wb.n + cnt > kCap) {
-        wb.thr = wave_compact(wb.buf, &wb.n, wb.K);
-        wb.thr_key = entry_key(wb.thr);
-        tf = key_float(wb.thr_key);
-        if (lane_id() == 0) atomicMax(wg_tau, wb.thr_key);
-#pragma unroll
-        for (int j = 0; j < V; j++) m[j] = ballot(((ok >> j) & 1u) && q[j] >= tf);
-    }
-#pragma unroll
-    for (int j = 0; j < V; j++) {
-        if (m[j]) {
-            if (((ok >> j) & 1u) && q[j] >= tf)
-                wb.buf[wb.n + lanes_below(m[j])] = make_entry(order_key(q[j]), (uint32_t) (i0 + j));
-            wb.n += (int) __popcll(m[j]);
-        }
-    }
-}
-
-// U vectors of V final logits per lane; vector u holds tokens i0[u] .. i0[u]+V-1. Bit j of live[u] is set where token
-// i0[u]+j is this lane's to take, and of ban[u] where that token is banned (its x is -inf). x of a token not live is
-// -inf or a copy of one taken elsewhere, so the group's largest x is a largest final logit. Every lane takes part.
-template <int U, int V>
-__device__ __forceinline__ void take_group(const Plan & pl, Lane & ln, WaveBuf & wb, uint32_t * wg_tau,
-                                           const float (&x)[U][V], const uint32_t (&live)[U], const uint32_t (&ban)[U],
-                                           const int (&i0)[U]) {
-    float gx = -INFINITY;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-#pragma unroll
-        for (int j = 0; j < V; j++) gx = fmaxf(gx, x[u][j]);
-    }
-    ln.mx = fmaxf(ln.mx, gx);
-    if (pl.flavor == SPX_FLAVOR_FISH) {
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-#pragma unroll
-            for (int j = 0; j < V; j++) ln.mn = fminf(ln.mn, ((live[u] >> j) & 1u) ? x[u][j] : INFINITY);
-        }
-    }
-    if (pl.mode == kGreedy) {
-        // tokens come to a lane by rising id: the first largest is the first strictly above all before it
-#pragma unroll
-        for (int u = 0; u < U; u++) {
-#pragma unroll
-            for (int j = 0; j < V; j++) {
-                if (((live[u] >> j) & 1u) && x[u][j] > ln.bestx) {
-                    ln.bestx = x[u][j];
-                    ln.besti = i0[u] + j;
-                }
-                if (((live[u] >> j) & 1u) && __builtin_isnan(x[u][j])) ln.flags |= kNaN;
-            }
-        }
-        return;
-    }
-    if (pl.need_s) {
-        // The wave's reference for the sum of exp: its largest quotient so far. Division by t > 0 rounded to nearest
-        // keeps the order, so the group's largest quotient is its largest logit divided.
-        const float wx = wave_max_f32(gx);
-        if (wx > -INFINITY) {
-            const float wm = div_rn(wx, pl.t, pl.rt);
-            if (wm > ln.m) {
-                ln.s *= exp((double) ln.m - (double) wm);
-                ln.m = wm;
-            }
-        }
-    }
-    const uint32_t tk = max(wb.thr_key, *(volatile uint32_t *) wg_tau);
-    float tf = tk ? key_float(tk) : -INFINITY;
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-        const uint32_t act = live[u] & ~ban[u];  // tokens whose quotient is computed
-        float q[V];
-        uint32_t nan = 0;
-#pragma unroll
-        for (int j = 0; j < V; j++) {
-            // x / t by Markstein's correction, the IEEE division where the quotient leaves the normal range
-            const float xv = x[u][j];
-            const float q0 = xv * pl.rt;
-            float qq = __builtin_fmaf(__builtin_fmaf(-q0, pl.t, xv), pl.rt, q0);
-            const float aq = __builtin_fabsf(q0);
-            if (__builtin_expect(((act >> j) & 1u) && !(aq >= 0x1p-125f && aq < INFINITY), 0)) qq = xv / pl.t;
-            if (pl.flavor == SPX_FLAVOR_HARU && ((act >> j) & 1u) && __builtin_isfinite(xv) && !__builtin_isfinite(qq))
-                ln.flags |= kTempOver;
-            qq = ((act >> j) & 1u) ? qq : -INFINITY;
-            nan |= __builtin_isnan(qq) ? (1u << j) : 0u;
-            q[j] = qq;
-        }
-        if (nan) ln.flags |= kNaN;
-        const uint32_t ok = act & ~nan;
-        if (pl.need_low) {
-#pragma unroll
-            for (int j = 0; j < V; j++) {
-                // banned tokens are the last of the order, -inf
-                const float qv = ((ban[u] >> j) & 1u) ? -INFINITY : q[j];
-                if ((((ok | ban[u]) & live[u]) >> j & 1u) && qv <= ln.lowq) {
-                    ln.lowq = qv;
-                    ln.lowi = i0[u] + j;
-                }
-            }
-        }
-        if (pl.need_s) {
-#pragma unroll
-            for (int j = 0; j < V; j++) ln.s += (double) __builtin_amdgcn_exp2f((q[j] - ln.m) * 1.4426950408889634f);
-        }
-        offer_vec<V>(wb, wg_tau, q, ok, tf, i0[u]);
-    }
-}
-
-// The special tokens among V consecutive tokens at chunk offset `off`: a history token is set aside for the post-pass
-// (its raw logit to its slot, -inf in x, out of `live`), a banned one becomes -inf and is marked in `ban`.
-template <int V>
-__device__ __forceinline__ void special_vec(const Specials & sp, float (&x)[V], uint32_t & live, uint32_t & ban, int off,
-                                            bool in) {
-    const uint2 pair = in ? sp.bits[off >> 5] : make_uint2(0u, 0u);
-    const int sh = off & 31;
-    const uint32_t mask = (1u << V) - 1u;
-    const uint32_t nh = (pair.x >> sh) & mask, nb = (pair.y >> sh) & mask & ~nh;
-    if (ballot(nh != 0)) {
-        if (nh) {
-            const int base = sp.rank[off >> 5];
-#pragma unroll
-            for (int j = 0; j < V; j++) {
-                if ((nh >> j) & 1u) sp.slot_raw[base + __popc(pair.x & ((1u << (sh + j)) - 1u))] = x[j];
-            }
-        }
-#pragma unroll
-        for (int j = 0; j < V; j++) x[j] = ((nh >> j) & 1u) ? -INFINITY : x[j];
-        live &= ~nh;
-    }
-    if (ballot(nb != 0)) {
-#pragma unroll
-        for (int j = 0; j < V; j++) x[j] = ((nb >> j) & 1u) ? -INFINITY : x[j];
-        ban = nb;
-    }
-}
-
-template <typename T, int B>
-__device__ __forceinline__ void stream_chunk(const Launch & a, const T * rowp, int c0, int c1, const Plan & pl,
-                                             const Specials & sp, Lane & ln, WaveBuf & wb, uint32_t * wg_tau) {
-    constexpr int V = Vec<T>::n;
-    const int n = c1 - c0;
-    const int tid = threadIdx.x;
-    int done = 0;
-    if (a.vec_ok) {
-        const int ng = n / V;  // whole vectors
-        const U32x4 * vp = (const U32x4 *) (rowp + c0);
-        // Four 16-byte loads in flight per lane before any is used; lanes past the end load the last vector again
-        // and take nothing from it.
-        for (int base = 0; base < ng; base += 4 * B) {
-            const int g0 = base + tid, g1 = g0 + B, g2 = g1 + B, g3 = g2 + B;
-            const U32x4 r0 = vp[min(g0, ng - 1)];
-            const U32x4 r1 = vp[min(g1, ng - 1)];
-            const U32x4 r2 = vp[min(g2, ng - 1)];
-            const U32x4 r3 = vp[min(g3, ng - 1)];
-            float x[4][V];
-            Vec<T>::unpack(r0, x[0]);
-            Vec<T>::unpack(r1, x[1]);
-            Vec<T>::unpack(r2, x[2]);
-            Vec<T>::unpack(r3, x[3]);
-            const int g[4] = {g0, g1, g2, g3};
-            uint32_t live[4], ban[4];
-            int i0[4];
-#pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const bool in = g[u] < ng;
-                live[u] = in ? (1u << V) - 1u : 0u;
-                ban[u] = 0u;
-                i0[u] = c0 + g[u] * V;
-                if (sp.any) special_vec<V>(sp, x[u], live[u], ban[u], g[u] * V, in);
-            }
-            take_group<4, V>(pl, ln, wb, wg_tau, x, live, ban, i0);
-        }
-        done = ng * V;
-    }
-    // One token per lane: a row that is not 16-byte aligned, and the tail of one that is.
-    for (int base = done; base < n; base += B) {
-        const int i = base + tid;
-        const bool in = i < n;
-        float x[1][1] = {{in ? load_one<T>(rowp + c0 + i) : -INFINITY}};
-        uint32_t live[1] = {in ? 1u : 0u}, ban[1] = {0u};
-        const int i0[1] = {c0 + i};
-        if (sp.any) special_vec<1>(sp, x[0], live[0], ban[0], i, in);
-        take_group<1, 1>(pl, ln, wb, wg_tau, x, live, ban, i0);
-    }
-}
-
-// The history tokens of the chunk, after the stream: penalties, the ban, then the same statistics.
-template <int B>
-__device__ __forceinline__ void take_specials(const spx_row_params & p, const Plan & pl, const Specials & sp,
-                                              const uint32_t * banned_row, Lane & ln, WaveBuf & wb, uint32_t * wg_tau) {
-    for (int base = 0; base < sp.n_slots; base += B) {
-        const int s = base + threadIdx.x;
-        const bool in = s < sp.n_slots;
-        float x[1][1] = {{-INFINITY}};
-        int i0[1] = {0};
-        uint32_t live[1] = {in ? 1u : 0u}, ban[1] = {0u};
-        if (in) {
-            const int id = sp.slot_id[s];
-            float v = penalize(sp.slot_raw[s], pl.counts ? sp.slot_cnt[s] : 0, p);
-            if (banned_row && ((banned_row[id >> 5] >> (id & 31)) & 1u)) {
-                v = -INFINITY;
-                ban[0] = 1u;
-            }
-            if (id == 0 && __builtin_isnan(v)) ln.flags |= kNaN0;
-            x[0][0] = v;
-            i0[0] = id;
-        }
-        take_group<1, 1>(pl, ln, wb, wg_tau, x, live, ban, i0);
-    }
-}
-
-// Reduces the lanes' states over the work-group, through LDS; every thread gets the totals.
-template <int B>
-__device__ inline RowTotals reduce_lanes(const Lane & ln, uint64_t * red64, double * redd, float * redf, uint32_t * redu) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    const uint64_t be = ln.besti >= 0 ? make_entry(order_key(ln.bestx), (uint32_t) ln.besti) : 0;
-    const uint64_t lo = ln.lowi >= 0 ? (((uint64_t) order_key(ln.lowq) << 32) | (uint64_t) (~(uint32_t) ln.lowi)) : ~0ull;
-    const uint64_t best = wave_max_u64(be);
-    const uint64_t low = wave_min_u64(lo);
-    const double s = wave_sum_f64(ln.s);  // m is the same in every lane of a wave
-    const float mx = wave_max_f32(ln.mx);
-    const float mn = -wave_max_f32(-ln.mn);
-    const uint32_t flags = wave_or_u32(ln.flags);
-    if (lane == 0) {
-        red64[2 * wave] = best;
-        red64[2 * wave + 1] = low;
-        redd[wave] = s;
-        redf[4 * wave] = ln.m;
-        redf[4 * wave + 1] = mx;
-        redf[4 * wave + 2] = mn;
-        redu[wave] = flags;
-    }
-    __syncthreads();
-    RowTotals t;
-    t.best = 0;
-    t.low = ~0ull;
-    t.m = -FLT_MAX;
-    t.mx = -INFINITY;
-    t.mn = INFINITY;
-    t.flags = 0;
-    t.s = 0;
-    for (int w = 0; w < B / kWave; w++) t.m = fmaxf(t.m, redf[4 * w]);
-    for (int w = 0; w < B / kWave; w++) {
-        t.best = red64[2 * w] > t.best ? red64[2 * w] : t.best;
-        t.low = red64[2 * w + 1] < t.low ? red64[2 * w + 1] : t.low;
-        t.flags |= redu[w];
-        t.mx = fmaxf(t.mx, redf[4 * w + 1]);
-        t.mn = fminf(t.mn, redf[4 * w + 2]);
-        t.s += redd[w] * ((redf[4 * w] == t.m) ? 1.0 : exp((double) redf[4 * w] - (double) t.m));
-    }
-    __syncthreads();
-    return t;
-}
-
-// Gathers the waves' entries at or above the largest of their K-th entries into dst (a power-of-two padded array),
-// sorts it, and returns how many of its first entries are real.
-template <int B>
-__device__ inline int union_and_sort(uint64_t * wave_bufs, const int * wave_n, const uint64_t * wave_thr, uint64_t * dst,
-                                     int cap, int * red) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    uint64_t floor = 0;
-    for (int w = 0; w < B / kWave; w++) floor = wave_thr[w] > floor ? wave_thr[w] : floor;
-    const int n = wave_n[wave];
-    const uint64_t * src = wave_bufs + wave * kCap;
-    int mine = 0;
-    for (int i0 = 0; i0 < n; i0 += kWave) mine += (int) __popcll(ballot(i0 + lane < n && src[i0 + lane] >= floor));
-    if (lane == 0) red[wave] = mine;
-    __syncthreads();
-    int base = 0, total = 0;
-    for (int w = 0; w < B / kWave; w++) {
-        if (w < wave) base += red[w];
-        total += red[w];
-    }
-    __syncthreads();
-    total = min(total, cap);
-    int pos = base;
-    for (int i0 = 0; i0 < n; i0 += kWave) {
-        const int i = i0 + lane;
-        const bool keep = i < n && src[i] >= floor;
-        const uint64_t m = ballot(keep);
-        if (keep && pos + lanes_below(m) < cap) dst[pos + lanes_below(m)] = src[i];
-        pos += (int) __popcll(m);
-    }
-    int np2 = 1;
-    while (np2 < total) np2 <<= 1;
-    for (int i = total + threadIdx.x; i < np2; i += B) dst[i] = 0;
-    __syncthreads();
-    block_sort_desc<B>(dst, np2);
-    return total;
-}
-
-__device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & split) {
-    // Work-groups are dispatched round-robin over the 8 XCDs; give the chunks of one row consecutive slots of one
-    // XCD, so that the partials the last chunk reads were written through the same L2.
-    const int x = bid & 7, l = bid >> 3;
-    const int per = nwg >> 3, extra = nwg & 7;
-    const int g = x * per + min(x, extra) + l;
-    row = g / splits;
-    split = g - row * splits;
-}
-
-
-// ------------------------------------------------------------------------------------------------------------------
 // The multi-pass path: exact radix selects over the whole row
 // ------------------------------------------------------------------------------------------------------------------
 
@@ -1004,6 +1129,8 @@ __device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & sp
 constexpr double kFix = 1099511627776.0;  // 2^40
 
 __device__ __forceinline__ uint64_t mass_fixed(float q, float top) {
+    // -inf weighs 0 (also against a top of -inf, where the reference's weights are NaN and pick() takes its last)
+    if (!(q > -INFINITY) || !(top > -INFINITY)) return 0;
     return (uint64_t) (exp((double) q - (double) top) * kFix + 0.5);
 }
 
@@ -1025,49 +1152,45 @@ struct FbRow {
     Specials sp;
     const uint32_t * banned_row;
     float top;  // the largest final quotient
-    int * ired;
+    Red * red;
 };
 
-// Visits every token's entry and fixed-point mass (a NaN quotient carries neither), chunk by chunk, each chunk's
-// special tokens rebuilt in LDS as the stream had them: a banned token as -inf, a history token by its final quotient.
+// Visits every token of the row, chunk by chunk, each chunk's special tokens rebuilt in LDS: f(entry, final logit,
+// quotient, banned, id), the entry 0 for a NaN quotient. A banned token is visited as -inf, once.
 template <typename T, int B, typename F>
 __device__ inline void fb_visit(FbRow & r, F && f) {
+    constexpr int V = Elt<T>::V;
     const Launch & a = *r.a;
     const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
     const bool spec = r.pl.pen || r.banned_row;
+    const uint32_t ninf = order_key(-INFINITY);
     for (int c0 = 0; c0 < a.vocab; c0 += a.chunk) {
         const int c1 = min(a.vocab, c0 + a.chunk);
         if (spec) {
             __syncthreads();  // the previous chunk's special tokens are read no more
             uint32_t bad = 0;
-            build_specials<B>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.ired, bad);
-            for (int s = threadIdx.x; s < r.sp.n_slots; s += B) {
-                const int id = r.sp.slot_id[s];
-                float v = penalize(load_one<T>(rowp + id), r.pl.counts ? r.sp.slot_cnt[s] : 0, r.p);
-                if (r.banned_row && ((r.banned_row[id >> 5] >> (id & 31)) & 1u)) v = -INFINITY;
-                r.sp.slot_raw[s] = div_rn(v, r.pl.t, r.pl.rt);  // from here on the final quotient
-            }
-            __syncthreads();
+            build_specials<B, V>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.red->i, bad);
         }
         for (int i = c0 + threadIdx.x; i < c1; i += B) {
-            float x;
             if (spec) {
-                const uint2 pair = r.sp.bits[(i - c0) >> 5];
-                const uint32_t bit = 1u << ((i - c0) & 31);
-                if (pair.x & bit) continue;
-                x = (pair.y & bit) ? -INFINITY : load_one<T>(rowp + i);
-            } else {
-                x = load_one<T>(rowp + i);
+                const int o = i - c0;
+                if ((r.sp.spec[o >> 5].x >> (o & 31)) & 1u) {
+                    // history tokens are visited below; a banned one (history or not) here
+                    if (r.banned_row && ((r.banned_row[i >> 5] >> (i & 31)) & 1u))
+                        f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
+                    continue;
+                }
             }
+            const float x = load_one<T>(rowp + i);
             const float q = div_rn(x, r.pl.t, r.pl.rt);
-            if (__builtin_isnan(q)) continue;
-            f(make_entry(order_key(q), (uint32_t) i), mass_fixed(q, r.top));
+            f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
         }
-        if (spec) {
-            for (int s = threadIdx.x; s < r.sp.n_slots; s += B) {
-                const float q = r.sp.slot_raw[s];
-                if (__builtin_isnan(q)) continue;
-                f(make_entry(order_key(q), (uint32_t) r.sp.slot_id[s]), mass_fixed(q, r.top));
+        if (r.pl.pen) {
+            for (int k = threadIdx.x; k < r.sp.n_slots * V; k += B) {
+                HistTok h;
+                if (!hist_token<T, V>(r.sp, k, c0, r.p, r.pl, r.banned_row, rowp, false, h) || h.banned) continue;
+                const float q = div_rn(h.v, r.pl.t, r.pl.rt);
+                f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) h.id), h.v, q, false, h.id);
             }
         }
     }
@@ -1079,14 +1202,14 @@ __device__ inline void fb_visit(FbRow & r, F && f) {
 template <typename T, int B>
 __device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool strict, Select & out,
                                  uint32_t * hist_n, unsigned long long * hist_m) {
-    int * ired = r.ired;
+    int * ired = r.red->i;
     Select s;
     s.prefix = 0;
     s.bits = 0;
     s.above_n = 0;
     s.above_m = 0;
     s.own_m = 0;
-    unsigned long long * shared = (unsigned long long *) (ired + 2);
+    unsigned long long * shared = (unsigned long long *) r.red->u;
     while (s.bits < 64) {
         for (int i = threadIdx.x; i < 256; i += B) {
             hist_n[i] = 0;
@@ -1096,11 +1219,13 @@ __device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool 
         const int shift = 56 - s.bits;
         const uint64_t pre = s.prefix;
         const int bits = s.bits;
-        fb_visit<T, B>(r, [&](uint64_t e, uint64_t w) {
+        const float top = r.top;
+        fb_visit<T, B>(r, [&](uint64_t e, float, float q, bool, int) {
+            if (!e) return;
             if (bits == 0 || (e >> (64 - bits)) == pre) {
                 const int d = (int) ((e >> shift) & 255u);
                 atomicAdd(&hist_n[d], 1u);
-                atomicAdd(&hist_m[d], (unsigned long long) w);
+                atomicAdd(&hist_m[d], (unsigned long long) mass_fixed(q, top));
             }
         });
         __syncthreads();
@@ -1138,13 +1263,14 @@ __device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool 
     return true;
 }
 
-// Resolves one row the one-pass path could not finish, in the row's last work-group, with radix selects over the
-// whole row (the candidate and sort regions of LDS are free by now).
+// Resolves one row the one-pass path could not finish, in a work-group of its own row, with exact passes over the
+// whole row: the flags and the row status, then radix selects. `extra` carries the flags found before (a history
+// longer than the handle allows).
 template <typename T, int B>
-__device__ inline void fallback_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl, uint64_t low,
-                                    float top, unsigned char * lds) {
+__device__ inline void fallback_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+                                    uint32_t extra, unsigned char * lds) {
     const int tid = threadIdx.x;
-    int * ired = (int *) (lds + a.off_red);
+    Red * red = (Red *) (lds + a.off_red);
     uint32_t * hist_n = (uint32_t *) (lds + a.off_sort);
     unsigned long long * hist_m = (unsigned long long *) (lds + a.off_sort + 1024);
     FbRow r;
@@ -1153,29 +1279,61 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     r.p = p;
     r.pl = pl;
     r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
-    r.sp.any = pl.pen || r.banned_row;
+    r.sp.spec = (uint2 *) (lds + a.off_spec);
+    r.sp.meta = (uint32_t *) (lds + a.off_meta);
+    r.sp.ufirst = (uint32_t *) (lds + a.off_ufirst);
+    r.sp.cnt = (uint32_t *) (lds + a.off_cnt);
+    r.sp.cap = lds + a.off_cap;
     r.sp.n_slots = 0;
-    r.sp.bits = (uint2 *) (lds + a.off_bits);
-    r.sp.rank = (int32_t *) (lds + a.off_rank);
-    r.sp.slot_id = (int32_t *) (lds + a.off_slots);
-    r.sp.slot_raw = (float *) (lds + a.off_slots + 4 * a.slot_cap);
-    r.sp.slot_cnt = (int32_t *) (lds + a.off_slots + 8 * a.slot_cap);
-    r.top = top;
-    r.ired = ired;
+    r.sp.any = pl.pen || r.banned_row;
+    r.top = 0.0f;
+    r.red = red;
+    // The flags, exactly, and the first and last entries of the order.
+    uint32_t fl = 0;
+    uint64_t hi_e = 0, lo_e = ~0ull;
+    fb_visit<T, B>(r, [&](uint64_t e, float v, float q, bool banned, int id) {
+        if (!banned) {
+            if (__builtin_isnan(v)) fl |= kNaN;
+            else if (v == INFINITY) fl |= kPosInf;
+            else if (v == -INFINITY) fl |= kNegInf;
+            else {
+                fl |= kFinite;
+                if (!__builtin_isfinite(q)) fl |= kTempOver;
+            }
+            if (id == 0 && __builtin_isnan(v)) fl |= kNaN0;
+        }
+        if (e) {
+            hi_e = e > hi_e ? e : hi_e;
+            lo_e = e < lo_e ? e : lo_e;
+        }
+    });
+    fl = block_or_u32<B>(fl, red->w) | (extra & kBadHist);
+    hi_e = block_max_u64<B>(hi_e, red->u);
+    lo_e = block_min_u64<B>(lo_e, red->u);
+    const bool top_finite = hi_e != 0 && __builtin_isfinite(entry_value(hi_e));
+    const int st = row_status(pl, p, fl, top_finite);
+    if (st >= 0) {
+        if (tid == 0) write_row(a, row, -1, st, 0);
+        return;
+    }
+    r.top = entry_value(hi_e);
     // The total mass over the row, as the selects count it.
-    unsigned long long * tot_m = (unsigned long long *) (ired + 8);
+    unsigned long long * tot_m = (unsigned long long *) &red->u[16];
     if (tid == 0) *tot_m = 0;
     __syncthreads();
     {
         unsigned long long mine = 0;
-        fb_visit<T, B>(r, [&](uint64_t, uint64_t w) { mine += w; });
+        const float top = r.top;
+        fb_visit<T, B>(r, [&](uint64_t e, float, float q, bool, int) {
+            if (e) mine += mass_fixed(q, top);
+        });
         atomicAdd(tot_m, mine);
     }
     __syncthreads();
     const uint64_t all_m = *tot_m;
     __syncthreads();
     const double u = a.u[row];
-    const int fl = pl.flavor;
+    const int fl_ = pl.flavor;
     auto sel = [&](bool by_mass, uint64_t target, bool strict, Select & out) {
         return fb_select<T, B>(r, by_mass, target, strict, out, hist_n, hist_m);
     };
@@ -1192,10 +1350,10 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     uint64_t kept_m = kmass, kept_n = kcount;
     Select scut;
     bool have_cut = false;
-    if (fl == SPX_FLAVOR_TRANSFORMERS || fl == SPX_FLAVOR_HARU) {
+    if (fl_ == SPX_FLAVOR_TRANSFORMERS || fl_ == SPX_FLAVOR_HARU) {
         // transformers keeps the token reaching top_p (qwen3-tts/sampler.cpp:92-96); torch's zeroing in
         // sample_token keeps the same prefix, the tokens after it weighing 0 (haru/sampler.cpp:52-59)
-        const bool applies = fl == SPX_FLAVOR_TRANSFORMERS ? pl.top_p < 1.0f : (pl.top_p > 0.0f && pl.top_p < 1.0f);
+        const bool applies = fl_ == SPX_FLAVOR_TRANSFORMERS ? pl.top_p < 1.0f : (pl.top_p > 0.0f && pl.top_p < 1.0f);
         if (applies) {
             const uint64_t target = (uint64_t) ((double) kmass * (double) pl.top_p + 0.5);
             if (sel(true, target, false, scut) && scut.above_n + 1 <= kcount) {
@@ -1220,10 +1378,10 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     const bool hit = sel(true, utarget, true, spk) && spk.above_n + 1 < kept_n;
     if (hit) {
         id = (int) entry_id(spk.entry);
-    } else if (fl == SPX_FLAVOR_HARU) {
+    } else if (fl_ == SPX_FLAVOR_HARU) {
         // pick() over all k weights, zeros included: the k-th token
-        id = have_k_entry ? (int) entry_id(sk.entry) : (int) ~(uint32_t) low;
-    } else if (have_cut && fl == SPX_FLAVOR_TRANSFORMERS) {
+        id = have_k_entry ? (int) entry_id(sk.entry) : (int) entry_id(lo_e);
+    } else if (have_cut && fl_ == SPX_FLAVOR_TRANSFORMERS) {
         id = (int) entry_id(scut.entry);
     } else if (have_cut) {
         Select sl;
@@ -1231,10 +1389,10 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     } else if (have_k_entry) {
         id = (int) entry_id(sk.entry);
     } else {
-        id = (int) ~(uint32_t) low;
+        id = (int) entry_id(lo_e);
     }
     if (tid == 0) {
-        write_row(a, row, id, SPX_ROW_OK, fl == SPX_FLAVOR_HARU ? pl.k : (int) kept_n);
+        write_row(a, row, id, SPX_ROW_OK, fl_ == SPX_FLAVOR_HARU ? pl.k : (int) kept_n);
         if (a.out_cand_ids) {
             // This path reports the id and the count of the kept candidates alone.
             for (int j = 0; j < a.max_out; j++) {
@@ -1246,11 +1404,347 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     }
 }
 
+// ------------------------------------------------------------------------------------------------------------------
+// Chunks and rows
+// ------------------------------------------------------------------------------------------------------------------
+
+__device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & split) {
+    // Work-groups are dispatched round-robin over the 8 XCDs; give the chunks of one row consecutive slots of one
+    // XCD, so that the partials the last chunk reads were written through the same L2.
+    const int x = bid & 7, l = bid >> 3;
+    const int per = nwg >> 3, extra = nwg & 7;
+    const int g = x * per + min(x, extra) + l;
+    row = g / splits;
+    split = g - row * splits;
+}
+
+// Counts this chunk in after its partial is published; true in the row's last chunk, whose threads then see every
+// partial of the row.
+template <int B>
+__device__ inline bool arrive_last(const Launch & a, int row, Ctl * ctl) {
+    __threadfence();  // this thread's part of the partial is visible device-wide
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const unsigned prev = atomicAdd(&a.counters[row], 1u);
+        const bool last = prev == (unsigned) (a.splits - 1);
+        if (last) a.counters[row] = 0;  // ready for the next launch
+        ctl->last = last ? 1u : 0u;
+    }
+    __syncthreads();
+    const bool last = ctl->last != 0;
+    if (last) __threadfence();  // the other chunks' partials are read after this
+    return last;
+}
+
+// Token 0's final logit, where it is not a history token, for std::max_element's NaN in front.
 template <typename T>
-__global__ __launch_bounds__(kBlock) void stream_kernel(Launch a) {
-    extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int B = kBlock;
+__device__ inline uint32_t nan0_flag(const T * rowp, const Plan & pl, const Specials & sp, const uint32_t * banned_row) {
+    const bool ban0 = banned_row && (banned_row[0] & 1u);
+    const bool hist0 = pl.pen && sp.any && (sp.spec[0].x & 1u) && !ban0;
+    if (ban0 || hist0) return 0u;
+    return __builtin_isnan(load_one<T>(rowp)) ? kNaN0 : 0u;
+}
+
+template <typename T, int B>
+__device__ inline void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
+                                  int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
+                                  uint32_t bad, unsigned char * lds) {
+    constexpr int V = Elt<T>::V;
+    constexpr int W = B / kWave;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    Ctl * ctl = (Ctl *) (lds + a.off_ctl);
+    Red * red = (Red *) (lds + a.off_red);
+    uint64_t * cand = (uint64_t *) (lds + a.off_cand);
+    uint64_t * sorted = (uint64_t *) (lds + a.off_sort);
+    const int cap = a.cand_cap;
+
+    SampleSt st;
+    st.s = 0.0;
+    st.m = -INFINITY;
+    st.hi = -FLT_MAX;
+    st.tau = -INFINITY;
+    st.lo = 0.0f;
+    st.inv = 0.0f;
+    st.delta = 0.0f;
+    st.hist_on = 0;
+    st.flags = 0;
+    GreedySt g;
+    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, cand, cap};
+    if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1);
+    else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1);
+
+    // The stream's totals: each wave's sum relative to its m, corrected for the rounding of m*L; then the chunk's.
+    {
+        double ws = wave_sum_f64(st.s);
+        if (st.m > -INFINITY) ws *= exp2(-(double) __builtin_fmaf(st.m, kL2e, -st.hi));
+        else ws = 0.0;
+        const uint32_t wf = wave_or_u32(st.flags);
+        const uint32_t f0 = (c0 == 0 && tid == 0) ? nan0_flag<T>(rowp, pl, sp, banned_row) : 0u;
+        if (lane == 0) {
+            red->d[wave] = ws;
+            red->f[wave] = st.m;
+            red->w[wave] = wf | f0;
+        }
+    }
+    __syncthreads();
+    float M = -INFINITY;
+    uint32_t F = bad;
+    for (int w = 0; w < W; w++) {
+        M = fmaxf(M, red->f[w]);
+        F |= red->w[w];
+    }
+    double S = 0.0;
+    for (int w = 0; w < W; w++)
+        if (red->f[w] > -INFINITY) S += red->d[w] * exp((double) red->f[w] - (double) M);
+    __syncthreads();
+
+    // The history tokens: penalties, the ban, then the same statistics and the same threshold.
+    if (pl.pen && sp.n_slots > 0) {
+        const int npairs = sp.n_slots * V;
+        float hm = -INFINITY;
+        uint32_t hf = 0;
+        for (int i = tid; i < npairs; i += B) {
+            HistTok h;
+            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h)) continue;
+            if (h.id == 0 && __builtin_isnan(h.v)) hf |= kNaN0;
+            if (h.banned) continue;
+            const float q = div_rn(h.v, pl.t, pl.rt);
+            if (__builtin_isnan(h.v)) hf |= kNaN;
+            else if (h.v == INFINITY) hf |= kPosInf;
+            else if (h.v == -INFINITY) hf |= kNegInf;
+            else {
+                hf |= kFinite;
+                if (!__builtin_isfinite(q)) hf |= kTempOver;
+            }
+            if (q > -INFINITY && q < INFINITY) hm = fmaxf(hm, q);
+        }
+        hm = block_max_f32<B>(hm, red->f);
+        F |= block_or_u32<B>(hf, red->w);
+        if (hm > M) {
+            if (M > -INFINITY) S *= exp((double) M - (double) hm);
+            M = hm;
+        }
+        const uint32_t tk = ctl->tau_key;
+        const float tau = tk ? key_float(tk) : -INFINITY;
+        double hs = 0.0;
+        for (int i = tid; i < npairs; i += B) {
+            HistTok h;
+            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h) || h.banned) continue;
+            const float q = div_rn(h.v, pl.t, pl.rt);
+            if (q > -INFINITY && q < INFINITY) hs += exp((double) q - (double) M);
+            if (!__builtin_isnan(q) && q >= tau) {
+                const uint32_t pos = atomicAdd(&ctl->n, 1u);
+                if (pos < (uint32_t) cap) cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
+                else ctl->overflow = 1u;
+            }
+        }
+        S += block_sum_f64<B>(hs, red->d);
+    }
+    // A finite quotient has a term above 0 against the largest one: S > 0. Every logit that is not finite, and every
+    // finite one whose quotient is not (the correction step gives NaN for both), went through the exact path, which
+    // set the flags.
+    if (S > 0.0) F |= kFinite;
+
+    // The candidates at or above the final threshold, sorted.
+    __syncthreads();
+    const uint32_t nres = ctl->n;
+    const bool overflow = ctl->overflow != 0 || nres > (uint32_t) cap;
+    const int nb = min((int) nres, cap);
+    const uint32_t tkey = ctl->tau_key;
+    const uint64_t floor = (uint64_t) tkey << 32;
+    const bool complete = tkey <= order_key(-INFINITY) && !overflow;  // the threshold never left -inf
+    int total = 0;
+    for (int i0 = 0; i0 < nb; i0 += B) {
+        const int i = i0 + tid;
+        const uint64_t e = i < nb ? cand[i] : 0ull;
+        const bool keep = e != 0 && e >= floor;
+        int cnt;
+        const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, red->i, cnt);
+        if (keep && total + pos < kSortCap) sorted[total + pos] = e;
+        total += cnt;
+    }
+    const bool too_many = total > kSortCap;
+    total = min(total, kSortCap);
+    {
+        int np2 = 1;
+        while (np2 < total) np2 <<= 1;
+        for (int i = total + tid; i < np2; i += B) sorted[i] = 0;
+        __syncthreads();
+        block_sort_desc<B>(sorted, np2);
+    }
+    const bool broken = overflow || too_many;
+
+    FinishLds L;
+    L.w = (double *) cand;
+    L.red = red->d;
+    L.ired = red->i;
+    L.pf = (float *) (cand + B);
+
+    if (a.splits == 1) {
+        RowTotals t{0ull, S, M, F};
+        if (broken || !finish_row<B>(a, row, p, pl, t, sorted, min(total, B), complete, L)) {
+            __syncthreads();
+            fallback_row<T, B>(a, row, p, pl, F, lds);
+        }
+        return;
+    }
+
+    // Publish this chunk's partial; the last chunk of the row to arrive merges them.
+    Partial * part = a.partials + (int64_t) row * a.splits + split;
+    uint64_t * pc = a.part_cands + ((int64_t) row * a.splits + split) * kKeep;
+    const int npub = min(total, kKeep);
+    for (int i = tid; i < npub; i += B) pc[i] = sorted[i];
+    if (tid == 0) {
+        part->best = 0;
+        part->floor = total > kKeep ? sorted[kKeep - 1] : floor;
+        part->s = S;
+        part->m = M;
+        part->flags = F;
+        part->n = npub;
+        part->complete = (complete && total <= kKeep) ? 1 : 0;
+        part->broken = broken ? 1 : 0;
+    }
+    if (!arrive_last<B>(a, row, ctl)) return;
+    RowTotals t{0ull, 0.0, -INFINITY, 0u};
+    uint64_t fl = 0;
+    bool all_complete = true, any_broken = false;
+    const Partial * pr = a.partials + (int64_t) row * a.splits;
+    for (int s2 = 0; s2 < a.splits; s2++) {
+        const Partial q = pr[s2];
+        t.flags |= q.flags;
+        t.m = fmaxf(t.m, q.m);
+        fl = q.floor > fl ? q.floor : fl;
+        all_complete = all_complete && q.complete;
+        any_broken = any_broken || q.broken;
+    }
+    for (int s2 = 0; s2 < a.splits; s2++) {
+        const Partial q = pr[s2];
+        if (q.m > -INFINITY) t.s += q.s * exp((double) q.m - (double) t.m);
+    }
+    if (t.s > 0.0) t.flags |= kFinite;
+    int tot = 0;
+    if (!any_broken) {
+        for (int s2 = 0; s2 < a.splits; s2++) {
+            const int ns = pr[s2].n;
+            const uint64_t * src = a.part_cands + ((int64_t) row * a.splits + s2) * kKeep;
+            for (int i0 = 0; i0 < ns; i0 += B) {
+                const int i = i0 + tid;
+                const bool keep = i < ns && src[i] >= fl;
+                int cnt;
+                const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, red->i, cnt);
+                if (keep && tot + pos < kSortCap) sorted[tot + pos] = src[i];
+                tot += cnt;
+            }
+        }
+        tot = min(tot, kSortCap);
+        int np2 = 1;
+        while (np2 < tot) np2 <<= 1;
+        for (int i = tot + tid; i < np2; i += B) sorted[i] = 0;
+        __syncthreads();
+        block_sort_desc<B>(sorted, np2);
+    }
+    if (any_broken || !finish_row<B>(a, row, p, pl, t, sorted, min(tot, B), all_complete, L)) {
+        __syncthreads();
+        fallback_row<T, B>(a, row, p, pl, t.flags, lds);
+    }
+}
+
+template <typename T, int B>
+__device__ inline void greedy_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
+                                  int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
+                                  uint32_t bad, unsigned char * lds) {
+    constexpr int V = Elt<T>::V;
+    constexpr int W = B / kWave;
+    const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
+    Ctl * ctl = (Ctl *) (lds + a.off_ctl);
+    Red * red = (Red *) (lds + a.off_red);
+
+    GreedySt g;
+    g.bx = -INFINITY;
+    g.bi = -1;
+    g.xmin = INFINITY;
+    g.nanb = 0;
+    SampleSt st;
+    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, nullptr, 0};
+    if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1);
+    else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1);
+
+    {
+        const uint64_t be = g.bi >= 0 ? make_entry(order_key(g.bx), (uint32_t) g.bi) : 0ull;
+        const uint64_t wb = wave_max_u64(be);
+        const float wx = -wave_max_f32(-g.xmin);
+        const uint32_t f0 = (c0 == 0 && tid == 0) ? nan0_flag<T>(rowp, pl, sp, banned_row) : 0u;
+        if (lane == 0) {
+            red->u[wave] = wb;
+            red->f[wave] = wx;
+            red->w[wave] = (g.nanb ? kNaN : 0u) | f0;
+        }
+    }
+    __syncthreads();
+    uint64_t best = 0;
+    float xmin = INFINITY;
+    uint32_t F = bad;
+    for (int w = 0; w < W; w++) {
+        best = red->u[w] > best ? red->u[w] : best;
+        xmin = fminf(xmin, red->f[w]);
+        F |= red->w[w];
+    }
+    __syncthreads();
+    if (pl.pen && sp.n_slots > 0) {
+        uint64_t hb = 0;
+        uint32_t hf = 0;
+        for (int i = tid; i < sp.n_slots * V; i += B) {
+            HistTok h;
+            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h)) continue;
+            if (h.id == 0 && __builtin_isnan(h.v)) hf |= kNaN0;
+            if (h.banned) continue;
+            if (__builtin_isnan(h.v)) hf |= kNaN;
+            else if (h.v == -INFINITY) hf |= kNegInf;
+            else {
+                const uint64_t e = make_entry(order_key(h.v), (uint32_t) h.id);
+                hb = e > hb ? e : hb;
+            }
+        }
+        const uint64_t b2 = block_max_u64<B>(hb, red->u);
+        best = b2 > best ? b2 : best;
+        F |= block_or_u32<B>(hf, red->w);
+    }
+    if (pl.xmin && xmin == -INFINITY) F |= kNegInf;
+
+    FinishLds L;
+    L.w = nullptr;
+    L.red = red->d;
+    L.ired = red->i;
+    L.pf = nullptr;
+    if (a.splits == 1) {
+        RowTotals t{best, 0.0, 0.0f, F | best_flags(best)};
+        finish_row<B>(a, row, p, pl, t, nullptr, 0, true, L);
+        return;
+    }
+    Partial * part = a.partials + (int64_t) row * a.splits + split;
+    if (tid == 0) {
+        part->best = best;
+        part->flags = F;
+        part->n = 0;
+        part->broken = 0;
+    }
+    if (!arrive_last<B>(a, row, ctl)) return;
+    RowTotals t{0ull, 0.0, 0.0f, 0u};
+    const Partial * pr = a.partials + (int64_t) row * a.splits;
+    for (int s2 = 0; s2 < a.splits; s2++) {
+        const Partial q = pr[s2];
+        t.best = q.best > t.best ? q.best : t.best;
+        t.flags |= q.flags;
+    }
+    t.flags |= best_flags(t.best);
+    finish_row<B>(a, row, p, pl, t, nullptr, 0, true, L);
+}
+
+template <typename T, int B>
+__global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    constexpr int V = Elt<T>::V;
+    const int tid = threadIdx.x;
     int row, split;
     xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
     if (row >= a.rows) return;
@@ -1270,210 +1764,73 @@ __global__ __launch_bounds__(kBlock) void stream_kernel(Launch a) {
         p.frequency_penalty = 0.0f;
     }
     const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr);
+    if (pl.mode == kInvalid) {
+        if (split == 0 && tid == 0) write_row(a, row, -1, SPX_ROW_INVALID_PARAMS, 0);
+        return;
+    }
     const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
     const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
     const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
+    Ctl * ctl = (Ctl *) (lds + a.off_ctl);
+    Red * red = (Red *) (lds + a.off_red);
+    const bool sampling = pl.mode != kGreedy;
 
-    int * ired = (int *) (lds + a.off_red);
-    double * dred = (double *) (lds + a.off_red + 256);
-    uint64_t * red64 = (uint64_t *) (lds + a.off_red + 512);
-    float * fred = (float *) (lds + a.off_red + 768);
-    uint32_t * ured = (uint32_t *) (lds + a.off_red + 1024);
-    int * wave_n = (int *) (lds + a.off_red + 1088);
-    uint64_t * wave_thr = (uint64_t *) (lds + a.off_red + 1152);
-    uint32_t * wg_tau = (uint32_t *) (ired + 60);  // the largest K-th key any wave has published
-
-    Lane ln;
-    lane_init(ln);
+    if (tid == 0) {
+        ctl->n = 0;
+        ctl->tau_key = 0;
+        ctl->overflow = 0;
+        ctl->last = 0;
+    }
+    if (tid < kBuckets) ctl->hist[tid] = 0;
+    if (sampling) {
+        uint64_t * cand = (uint64_t *) (lds + a.off_cand);
+        for (int i = tid; i < a.cand_cap; i += B) cand[i] = 0;
+    }
     Specials sp;
-    sp.any = false;
+    sp.spec = (uint2 *) (lds + a.off_spec);
+    sp.meta = (uint32_t *) (lds + a.off_meta);
+    sp.ufirst = (uint32_t *) (lds + a.off_ufirst);
+    sp.cnt = (uint32_t *) (lds + a.off_cnt);
+    sp.cap = lds + a.off_cap;
     sp.n_slots = 0;
-    sp.bits = (uint2 *) (lds + a.off_bits);
-    sp.rank = (int32_t *) (lds + a.off_rank);
-    sp.slot_id = (int32_t *) (lds + a.off_slots);
-    sp.slot_raw = (float *) (lds + a.off_slots + 4 * a.slot_cap);
-    sp.slot_cnt = (int32_t *) (lds + a.off_slots + 8 * a.slot_cap);
+    sp.any = pl.pen || banned_row != nullptr;
     uint32_t bad = 0;
-    if (tid == 0) *wg_tau = 0;
-    if (pl.mode != kInvalid && (pl.pen || banned_row)) {
-        sp.any = true;
-        build_specials<B>(sp, a, row, c0, c1, pl, banned_row, ired, bad);
-    }
+    if (sp.any) build_specials<B, V>(sp, a, row, c0, c1, pl, banned_row, red->i, bad);
     __syncthreads();
-    ln.flags |= bad;
-
-    const bool sampling = pl.mode == kTopK || pl.mode == kFull;
-    WaveBuf wb;
-    wb.buf = (uint64_t *) (lds + a.off_cand) + wave * kCap;
-    wb.n = 0;
-    wb.thr = 0;
-    wb.thr_key = 0;
-    wb.K = pl.kc;
-
-    if (pl.mode != kInvalid) {
-        stream_chunk<T, B>(a, rowp, c0, c1, pl, sp, ln, wb, wg_tau);
-        // Token 0, where it is not a history token, for std::max_element's NaN in front.
-        if (c0 == 0 && tid == 0) {
-            const uint2 pair = sp.any ? sp.bits[0] : make_uint2(0u, 0u);
-            if (!(pair.x & 1u)) {
-                const float x0 = (pair.y & 1u) ? -INFINITY : load_one<T>(rowp);
-                if (__builtin_isnan(x0)) ln.flags |= kNaN0;
-            }
-        }
-        if (sp.any) {
-            __syncthreads();
-            take_specials<B>(p, pl, sp, banned_row, ln, wb, wg_tau);
-        }
-    }
-
-    // Each wave keeps exactly its top K; its K-th entry bounds the row's K-th from below.
-    uint64_t thr = 0;
-    if (sampling) {
-        if (wb.n > wb.K) {
-            thr = wave_compact(wb.buf, &wb.n, wb.K);
-        } else if (wb.n == wb.K) {
-            uint64_t m = ~0ull;
-            for (int i = lane; i < wb.n; i += kWave) m = wb.buf[i] < m ? wb.buf[i] : m;
-            thr = wave_min_u64(m);
-        }
-    }
-    if (lane == 0) {
-        wave_n[wave] = sampling ? wb.n : 0;
-        wave_thr[wave] = thr;
-    }
-    const RowTotals tot = reduce_lanes<B>(ln, red64, dred, fred, ured);  // its barriers publish wave_n
-
-    uint64_t * sorted = (uint64_t *) (lds + a.off_sort);
-    int n = 0;
-    bool complete = true;
-    if (sampling) {
-        n = union_and_sort<B>((uint64_t *) (lds + a.off_cand), wave_n, wave_thr, sorted, a.sort_cap, ired);
-        complete = n < pl.kc;  // fewer than K: no wave ever dropped an entry
-        n = min(n, pl.kc);
-    }
-
-    FinishLds L;
-    L.w = (double *) (lds + a.off_cand);
-    L.red = dred;
-    L.ired = ired;
-    L.pf = (float *) (lds + a.off_cand + 8 * kKeep);
-
-    if (a.splits > 1) {
-        // Publish this chunk's partial; the last chunk of the row to arrive merges them.
-        Partial * part = a.partials + (int64_t) row * a.splits + split;
-        uint64_t * pc = a.part_cands + ((int64_t) row * a.splits + split) * kKeep;
-        for (int i = tid; i < n; i += B) pc[i] = sorted[i];
-        if (tid == 0) {
-            part->best = tot.best;
-            part->low = tot.low;
-            part->s = tot.s;
-            part->m = tot.m;
-            part->mx = tot.mx;
-            part->mn = tot.mn;
-            part->flags = tot.flags;
-            part->n = n;
-            part->complete = complete ? 1 : 0;
-            part->kth = (n >= pl.kc && n > 0) ? sorted[n - 1] : 0;
-        }
-        // One wave makes the partial visible device-wide and counts the chunk in; the last chunk's first wave makes
-        // the others' visible to its work-group.
-        __syncthreads();
-        if (tid == 0) {
-            __threadfence();
-            const unsigned prev = atomicAdd(&a.counters[row], 1u);
-            const int last = prev == (unsigned) (a.splits - 1);
-            if (last) {
-                __threadfence();
-                a.counters[row] = 0;  // ready for the next launch
-            }
-            ired[0] = last;
-        }
-        __syncthreads();
-        if (!ired[0]) return;
-        RowTotals t;
-        t.best = 0;
-        t.low = ~0ull;
-        t.flags = 0;
-        t.m = -FLT_MAX;
-        t.mx = -INFINITY;
-        t.mn = INFINITY;
-        t.s = 0;
-        uint64_t floor = 0;
-        bool all_complete = true;
-        const Partial * pr = a.partials + (int64_t) row * a.splits;
-        for (int s2 = 0; s2 < a.splits; s2++) {
-            const Partial q = pr[s2];
-            t.best = q.best > t.best ? q.best : t.best;
-            t.low = q.low < t.low ? q.low : t.low;
-            t.flags |= q.flags;
-            t.m = fmaxf(t.m, q.m);
-            t.mx = fmaxf(t.mx, q.mx);
-            t.mn = fminf(t.mn, q.mn);
-            floor = q.kth > floor ? q.kth : floor;
-            all_complete = all_complete && q.complete;
-        }
-        for (int s2 = 0; s2 < a.splits; s2++) {
-            const Partial q = pr[s2];
-            t.s += q.s * ((q.m == t.m) ? 1.0 : exp((double) q.m - (double) t.m));
-        }
-        int total = 0;
-        if (sampling) {
-            for (int s2 = 0; s2 < a.splits; s2++) {
-                const int ns = pr[s2].n;
-                const uint64_t * src = a.part_cands + ((int64_t) row * a.splits + s2) * kKeep;
-                for (int i0 = 0; i0 < ns; i0 += B) {
-                    const int i = i0 + tid;
-                    const bool keep = i < ns && src[i] >= floor;
-                    int cnt_total;
-                    const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, ired + 32, cnt_total);
-                    if (keep && total + pos < a.sort_cap) sorted[total + pos] = src[i];
-                    total += cnt_total;
-                }
-            }
-            total = min(total, a.sort_cap);
-            int np2 = 1;
-            while (np2 < total) np2 <<= 1;
-            for (int i = total + tid; i < np2; i += B) sorted[i] = 0;
-            __syncthreads();
-            block_sort_desc<B>(sorted, np2);
-        }
-        n = min(total, pl.kc);
-        if (!finish_row<B>(a, row, p, pl, t, sorted, n, all_complete, L)) {
-            const float top = entry_value(sorted[0]);
-            __syncthreads();
-            fallback_row<T, B>(a, row, p, pl, t.low, top, lds);
-        }
-        return;
-    }
-    if (!finish_row<B>(a, row, p, pl, tot, sorted, n, complete, L)) {
-        const float top = entry_value(sorted[0]);
-        __syncthreads();
-        fallback_row<T, B>(a, row, p, pl, tot.low, top, lds);
-    }
+    if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds);
+    else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
 // Launchers
 // ------------------------------------------------------------------------------------------------------------------
 
-hipError_t launch_stream(const Launch & a, hipStream_t s) {
+hipError_t launch_sampler(const Launch & a, hipStream_t s) {
     if (a.nwg == 0) return hipSuccess;
-    if (a.dtype == SPX_BF16) {
-        hipLaunchKernelGGL(stream_kernel<uint16_t>, dim3(a.nwg), dim3(kBlock), a.lds_bytes, s, a);
+    if (a.block == kBlockBig) {
+        if (a.dtype == SPX_BF16)
+            hipLaunchKernelGGL((sampler_kernel<uint16_t, kBlockBig>), dim3(a.nwg), dim3(kBlockBig), a.lds_bytes, s, a);
+        else
+            hipLaunchKernelGGL((sampler_kernel<float, kBlockBig>), dim3(a.nwg), dim3(kBlockBig), a.lds_bytes, s, a);
     } else {
-        hipLaunchKernelGGL(stream_kernel<float>, dim3(a.nwg), dim3(kBlock), a.lds_bytes, s, a);
+        if (a.dtype == SPX_BF16)
+            hipLaunchKernelGGL((sampler_kernel<uint16_t, kBlockSmall>), dim3(a.nwg), dim3(kBlockSmall), a.lds_bytes, s, a);
+        else
+            hipLaunchKernelGGL((sampler_kernel<float, kBlockSmall>), dim3(a.nwg), dim3(kBlockSmall), a.lds_bytes, s, a);
     }
     return hipGetLastError();
 }
 
-hipError_t set_lds_limits(int stream_bytes) {
-    hipError_t e = hipSuccess;
-    if (stream_bytes > 65536) {
-        e = hipFuncSetAttribute((const void *) stream_kernel<float>, hipFuncAttributeMaxDynamicSharedMemorySize, stream_bytes);
-        if (e == hipSuccess)
-            e = hipFuncSetAttribute((const void *) stream_kernel<uint16_t>, hipFuncAttributeMaxDynamicSharedMemorySize, stream_bytes);
+hipError_t set_lds_limits(int bytes) {
+    if (bytes <= 65536) return hipSuccess;
+    const void * fns[4] = {(const void *) sampler_kernel<float, kBlockBig>, (const void *) sampler_kernel<uint16_t, kBlockBig>,
+                           (const void *) sampler_kernel<float, kBlockSmall>,
+                           (const void *) sampler_kernel<uint16_t, kBlockSmall>};
+    for (const void * f : fns) {
+        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+        if (e != hipSuccess) return e;
     }
-    return e;
+    return hipSuccess;
 }
 
 }  // namespace spx
