@@ -125,12 +125,15 @@ __device__ __forceinline__ double wave_incl_scan_f64(double v) {
     }
     return v;
 }
+// Inclusive prefix sum of ints over the wave's lanes through DPP (every lane active).
 __device__ __forceinline__ int wave_incl_scan_i32(int v) {
-    const int l = lane_id();
-    for (int d = 1; d < kWave; d <<= 1) {
-        const int o = __shfl_up(v, d, kWave);
-        if (l >= d) v += o;
-    }
+    // within each row of 16 lanes by shifts, then rows 1 and 3 add lane 15 of the row before, rows 2 and 3 lane 31
+    v += __builtin_amdgcn_update_dpp(0, v, 0x111, 0xf, 0xf, true);  // row_shr:1
+    v += __builtin_amdgcn_update_dpp(0, v, 0x112, 0xf, 0xf, true);  // row_shr:2
+    v += __builtin_amdgcn_update_dpp(0, v, 0x114, 0xf, 0xf, true);  // row_shr:4
+    v += __builtin_amdgcn_update_dpp(0, v, 0x118, 0xf, 0xf, true);  // row_shr:8
+    v += __builtin_amdgcn_update_dpp(0, v, 0x142, 0xa, 0xf, false); // row_bcast:15
+    v += __builtin_amdgcn_update_dpp(0, v, 0x143, 0xc, 0xf, false); // row_bcast:31
     return v;
 }
 

@@ -23,8 +23,6 @@ constexpr int kKeepFull = 128;
 constexpr int kSortCap = 1024;
 constexpr int kMaxSplits = 4;
 constexpr int kMaxSplitsGreedy = 16;
-// Buckets of the histogram that raises a chunk's threshold.
-constexpr int kBuckets = 128;
 // The largest history a handle takes: slot ranks are kept in 24 bits and the LDS must hold the slots.
 constexpr int kMaxHist = 4096;
 

@@ -166,42 +166,6 @@ __device__ inline int block_excl_scan_i32(int v, int * red, int & total) {
 }
 
 template <int B>
-__device__ inline double block_sum_f64(double v, double * red) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    v = wave_sum_f64(v);
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    double t = 0;
-    for (int w = 0; w < B / kWave; w++) t += red[w];
-    __syncthreads();
-    return t;
-}
-
-template <int B>
-__device__ inline double block_incl_scan_f64(double v, double * red) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    const double inc = wave_incl_scan_f64(v);
-    if (lane == kWave - 1) red[wave] = inc;
-    __syncthreads();
-    double base = 0;
-    for (int w = 0; w < wave; w++) base += red[w];
-    __syncthreads();
-    return base + inc;
-}
-
-template <int B>
-__device__ inline int block_min_i32(int v, int * red) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    v = (int) wave_reduce_u32((uint32_t) v, [](uint32_t a, uint32_t b) { return (int) a < (int) b ? a : b; });
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    int t = red[0];
-    for (int w = 1; w < B / kWave; w++) t = min(t, red[w]);
-    __syncthreads();
-    return t;
-}
-
-template <int B>
 __device__ inline uint32_t block_or_u32(uint32_t v, uint32_t * red) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     v = wave_or_u32(v);
@@ -209,18 +173,6 @@ __device__ inline uint32_t block_or_u32(uint32_t v, uint32_t * red) {
     __syncthreads();
     uint32_t t = 0;
     for (int w = 0; w < B / kWave; w++) t |= red[w];
-    __syncthreads();
-    return t;
-}
-
-template <int B>
-__device__ inline float block_max_f32(float v, float * red) {
-    const int lane = lane_id(), wave = threadIdx.x / kWave;
-    v = wave_max_f32(v);
-    if (lane == 0) red[wave] = v;
-    __syncthreads();
-    float t = -INFINITY;
-    for (int w = 0; w < B / kWave; w++) t = fmaxf(t, red[w]);
     __syncthreads();
     return t;
 }
@@ -249,35 +201,17 @@ __device__ inline uint64_t block_min_u64(uint64_t v, uint64_t * red) {
     return t;
 }
 
-// Sorts a[0..n) (n a power of two) into falling order, in LDS.
-template <int B>
-__device__ inline void block_sort_desc(uint64_t * a, int n) {
-    for (int size = 2; size <= n; size <<= 1) {
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            for (int t = threadIdx.x; t < (n >> 1); t += B) {
-                const int lo = 2 * t - (t & (stride - 1));
-                const int hi = lo + stride;
-                const bool desc = (lo & size) == 0;
-                const uint64_t x = a[lo], y = a[hi];
-                if ((x < y) == desc) {
-                    a[lo] = y;
-                    a[hi] = x;
-                }
-            }
-            __syncthreads();
-        }
-    }
-}
-
 // The control block of a chunk, in LDS.
 struct Ctl {
     uint32_t n;         // candidate entries reserved
     uint32_t tau_key;   // order key of the threshold (0: none yet)
     uint32_t overflow;  // entries were dropped for want of room
     uint32_t last;      // this work-group merges its row
+    uint32_t resolved;  // the finishing wave settled the row
+    uint32_t ncomp;     // candidates at or above the final threshold
+    uint32_t kkey;      // the chunk's K-th key
     float wave_t[16];   // per wave: its bound on the K-th quotient, and its largest quotient, of the first step
     float wave_m[16];
-    uint32_t hist[kBuckets];  // appended quotients by bucket of the threshold histogram
 };
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -351,9 +285,11 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
         nv += __popc(vec_mask<V>(h));
         nu += __popc(h);
     }
-    int tv, tu;
-    int vb = block_excl_scan_i32<B>(nv, red, tv);
-    int ub = block_excl_scan_i32<B>(nu, red, tu);
+    // one scan of both counts, each below 2^16 (a chunk holds at most max_hist <= kMaxHist history tokens)
+    int tot2;
+    const int base2 = block_excl_scan_i32<B>((nv << 16) | nu, red, tot2);
+    int vb = base2 >> 16, ub = base2 & 0xffff;
+    const int tv = tot2 >> 16, tu = tot2 & 0xffff;
     for (int w = w0; w < w1; w++) {
         const uint32_t h = sp.spec[w].y;
         const uint32_t occ = vec_mask<V>(h);
@@ -449,8 +385,6 @@ struct SampleSt {
     double s;        // lane: sum of 2^(q*L - hi) over its groups, L = log2(e) in float
     float m, hi;     // wave: the reference quotient and RN(m*L) (-FLT_MAX while no finite quotient is known)
     float tau;       // wave: a quotient at or above it enters the buffer
-    float lo, inv, delta;  // wave: the bucket map of the histogram, bucket b = (q - lo) * inv
-    int hist_on;
     uint32_t flags;  // lane
 };
 
@@ -489,11 +423,6 @@ __device__ __forceinline__ void bootstrap(const Plan & pl, SampleSt & st, Ctl * 
     st.tau = tau0;
     st.m = mref;
     st.hi = mref > -INFINITY ? mref * kL2e : -FLT_MAX;
-    const float span = mref - tau0;
-    st.hist_on = (tau0 > -INFINITY && span > 0.0f && span < INFINITY) ? 1 : 0;
-    st.lo = tau0;
-    st.inv = st.hist_on ? 120.0f / span : 0.0f;
-    st.delta = st.hist_on ? span / 120.0f : 0.0f;
     if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tau0));
 }
 
@@ -534,28 +463,11 @@ __device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE]
     st.s += (double) acc;
 }
 
-// A bound on the K-th appended quotient from the histogram: the boundary of the highest bucket with at least K
-// appended quotients at or above it, less one bucket (the float rounding of (q - lo) * inv cannot move a counted
-// quotient under it); -inf when there is none.
-__device__ __forceinline__ float hist_bound(const uint32_t * hist, int K, float lo, float delta) {
-    const int l = lane_id();
-    const uint32_t ha = hist[kBuckets - 1 - 2 * l], hb = hist[kBuckets - 2 - 2 * l];
-    const int incl = wave_incl_scan_i32((int) (ha + hb));  // appended at or above bucket kBuckets-2-2l
-    const uint64_t ge = ballot(incl >= K);
-    if (!ge) return -INFINITY;
-    const int l0 = (int) __builtin_ctzll(ge);
-    const int in0 = __builtin_amdgcn_readlane(incl, l0), hb0 = __builtin_amdgcn_readlane((int) hb, l0);
-    const int bstar = (in0 - hb0 >= K) ? kBuckets - 1 - 2 * l0 : kBuckets - 2 - 2 * l0;
-    if (bstar < 2) return -INFINITY;
-    return lo + (float) (bstar - 1) * delta;
-}
-
-// The K-th largest key among the first `lim` entries of the buffer (entries other waves have reserved but not
-// written yet read as 0 and are not counted); 0 when there are fewer than K. Taken when the buffer fills past a half
-// and three quarters, which happens where the histogram has no range (no bound from the first step) or the logits
-// come in rising order.
+// The K-th largest key among the first `lim` entries of the buffer, by one wave (entries other waves have reserved
+// but not written yet read as 0 and are not counted); 0 when there are fewer than K. A bitwise search from the top
+// key bit down, each step counting the keys at or above the candidate with one ballot count per register.
 __device__ __forceinline__ uint32_t buffer_bound(const uint64_t * cand, int lim, int K) {
-    constexpr int kMaxPerLane = 24;  // lim <= 3/4 of a buffer of 2048 entries
+    constexpr int kMaxPerLane = 32;  // lim <= a buffer of 2048 entries
     const int l = lane_id();
     uint32_t keys[kMaxPerLane];
 #pragma unroll
@@ -574,54 +486,48 @@ __device__ __forceinline__ uint32_t buffer_bound(const uint64_t * cand, int lim,
     return key;
 }
 
-// Appends the lanes' passing quotients to the buffer: each lane writes its own run, placed by a scan over the wave;
-// one atomic per wave reserves the room. `all` (no bound yet) takes every valid element, -inf ones included.
+// Appends the passing elements of a step to the buffer: a ballot per element, one atomic per wave for the room,
+// each passing lane writing at its rank within its element's ballot. `all` (no bound yet) takes every valid element,
+// -inf ones included. The wave whose appends pass a multiple of 128 entries raises the work-group's threshold to the
+// K-th key of the buffer so far; every wave takes it up at its next step.
 template <int B, int VV, bool MASK>
 __device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
-                                            const float (&q)[kE], const float (&x)[kE], uint32_t kill, int id_base) {
-    const bool all = !(st.tau > -INFINITY);
-    uint32_t pass = 0;
+                                               const float (&q)[kE], const float (&x)[kE], uint32_t kill, int id_base,
+                                               bool all) {
+    uint64_t pm[kE];
+    int total = 0;
 #pragma unroll
     for (int k = 0; k < kE; k++) {
         const bool live = !MASK || !((kill >> k) & 1u);
-        const bool p = all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau);
-        pass |= p ? (1u << k) : 0u;
+        pm[k] = ballot(all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau));
+        total += (int) __popcll(pm[k]);
     }
-    const int c = __popc(pass);
-    const int incl = wave_incl_scan_i32(c);
-    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
+    if (total == 0) return;
     uint32_t base = 0;
     if (lane_id() == 0) base = atomicAdd(&ctl->n, (uint32_t) total);
     base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
     if (base + (uint32_t) total > (uint32_t) cap && lane_id() == 0) ctl->overflow = 1u;
-    int pos = (int) base + incl - c;
+    int off = (int) base;
 #pragma unroll
     for (int k = 0; k < kE; k++) {
-        if ((pass >> k) & 1u) {
-            if (pos < cap) {
-                // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
-                float qq = q[k];
-                if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = x[k] / pl.t;
-                const int id = id_base + (k / VV) * (B * VV) + (k % VV);
-                cand[pos] = make_entry(order_key(qq), (uint32_t) id);
-                if (st.hist_on) {
-                    const float bf = fminf((qq - st.lo) * st.inv, (float) (kBuckets - 1));
-                    atomicAdd(&ctl->hist[max((int) bf, 0)], 1u);
+        if (pm[k]) {
+            if ((pm[k] >> lane_id()) & 1ull) {
+                const int pos = off + lanes_below(pm[k]);
+                if (pos < cap) {
+                    // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
+                    float qq = q[k];
+                    if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = x[k] / pl.t;
+                    const int id = id_base + (k / VV) * (B * VV) + (k % VV);
+                    cand[pos] = make_entry(order_key(qq), (uint32_t) id);
                 }
             }
-            pos++;
+            off += (int) __popcll(pm[k]);
         }
     }
     const uint32_t end = base + (uint32_t) total;
-    const uint32_t l1 = (uint32_t) cap / 2, l2 = (uint32_t) cap / 4 * 3;
-    float tn = -INFINITY;
-    if ((base < l1 && end >= l1) || (base < l2 && end >= l2)) {
-        const uint32_t kk = buffer_bound(cand, (int) (base < l1 ? l1 : l2), pl.K);
-        if (kk) tn = key_float(kk);
-    } else if (st.hist_on) {
-        tn = hist_bound(ctl->hist, pl.K, st.lo, st.delta);
-    }
-    tn = uniform_f(tn);
+    if ((base >> 7) == (end >> 7)) return;
+    const uint32_t kk = buffer_bound(cand, min((int) (end & ~127u), cap), pl.K);
+    const float tn = uniform_f(kk ? key_float(kk) : -INFINITY);
     if (tn > st.tau) {
         st.tau = tn;
         if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tn));
@@ -645,6 +551,8 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
         for (int k = 0; k < kE; k++) q[k] = kill_to(q[k], kill, k);
     }
     if (BOOT) bootstrap<B>(pl, st, ctl, q);
+    // the work-group's threshold, raised by whichever wave last refreshed it
+    const uint32_t tk = BOOT ? 0u : __hip_atomic_load(&ctl->tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
     float t[kE];
 #pragma unroll
     for (int k = 0; k < kE; k++) t[k] = __builtin_amdgcn_exp2f(__builtin_fmaf(q[k], kL2e, -st.hi));
@@ -655,22 +563,17 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
     }
     if (ballot(!(t[0] <= 0x1p100f))) slow_group(pl, st, q, x, kill, MASK);
     else st.s += (double) t[0];
-    // Candidates: the lane's largest quotient against tau first (NaN never passes), the lanes' runs only then.
-    bool any;
+    if (!BOOT && tk) st.tau = fmaxf(st.tau, uniform_f(key_float(tk)));
+    // Candidates: one ballot per element against tau (NaN never passes); the appends only where a lane passes.
     if (st.tau > -INFINITY) {
-        float tq[kE];
+        uint64_t any = 0;
 #pragma unroll
-        for (int k = 0; k < kE; k++) tq[k] = q[k];
-#pragma unroll
-        for (int w = kE / 2; w >= 1; w >>= 1) {
-#pragma unroll
-            for (int k = 0; k < w; k++) tq[k] = fmaxf(tq[k], tq[k + w]);
-        }
-        any = ballot(tq[0] >= st.tau) != 0;
+        for (int k = 0; k < kE; k++) any |= ballot(q[k] >= st.tau);
+        if (any) insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base, false);
     } else {
-        any = true;
+        // no bound yet: every valid token of the chunk enters
+        insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base, true);
     }
-    if (any) insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -762,6 +665,20 @@ __device__ __forceinline__ void run_core(StreamCtx & c, const float (&x)[kE], ui
     else sample_core<B, VV, MASK, BOOT>(*c.pl, *c.st, c.ctl, c.cand, c.cap, x, kill, rdead, id_base);
 }
 
+// The first step's vectors of a chunk (lanes past the last whole vector load it again; none when there is none).
+template <typename T, int B>
+__device__ inline void load_first(const Launch & a, const T * rowp, int c0, int c1, U32x4 (&first)[Elt<T>::U]) {
+    constexpr int V = Elt<T>::V, U = Elt<T>::U;
+    const int ng = a.vec_ok ? (c1 - c0) / V : 0;
+    const U32x4 * vp = (const U32x4 *) (rowp + c0);
+#pragma unroll
+    for (int u = 0; u < U; u++) first[u] = U32x4{0u, 0u, 0u, 0u};
+    if (ng > 0) {
+#pragma unroll
+        for (int u = 0; u < U; u++) first[u] = vp[min((int) threadIdx.x + u * B, ng - 1)];
+    }
+}
+
 // kE tokens per lane, one each at chunk offsets o0 + k*B: rows that are not 16-byte aligned, and a chunk's tail.
 template <typename T, int B, bool SPEC, bool GREEDY, bool BOOT>
 __device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int c0, int n, int o0) {
@@ -826,7 +743,8 @@ __device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T
 }
 
 template <typename T, int B, bool SPEC, bool GREEDY>
-__device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * rowp, int c0, int c1) {
+__device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * rowp, int c0, int c1,
+                                    const U32x4 (&first)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V, U = Elt<T>::U;
     const int n = c1 - c0, tid = threadIdx.x;
     if (!a.vec_ok) {
@@ -846,12 +764,8 @@ __device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * r
     U32x4 cur[U], nxt[U];
 #pragma unroll
     for (int u = 0; u < U; u++) {
-        cur[u] = U32x4{0u, 0u, 0u, 0u};
+        cur[u] = first[u];  // loaded before the special tokens were built
         nxt[u] = cur[u];
-    }
-    if (ng > 0) {
-#pragma unroll
-        for (int u = 0; u < U; u++) cur[u] = vp[min(tid + u * B, gl)];
     }
     if (nit > 1) {
 #pragma unroll
@@ -923,39 +837,58 @@ __device__ inline uint32_t best_flags(uint64_t best) {
     return v == INFINITY ? kPosInf : (v > -INFINITY ? kFinite : 0u);
 }
 
-// Scratch of the finishing step, in LDS.
-struct FinishLds {
-    double * w;   // weights, up to B
-    double * red;
-    int * ired;
-    float * pf;   // float weights (HARU), up to B
-};
-
 constexpr int kNone = 0x7fffffff;
+// Entries the finishing wave takes: four per lane.
+constexpr int kFinishMax = 4 * kWave;
 
-// Finishes a row from its totals and its n sorted top entries e[0..n), n <= B. Returns true when the row is done,
-// false when it needs the multi-pass path (its top-p set or its draw runs beyond the entries held).
-template <int B>
-__device__ inline bool finish_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
-                                  const RowTotals & tot, const uint64_t * e, int n, bool complete, FinishLds & L) {
-    const int tid = threadIdx.x;
+// Helpers of the finishing wave: element i of a row's sorted entries sits in lane i/4, slot i%4.
+struct Cum4 {
+    double c[4];
+};
+// Inclusive running sums over the elements in their order.
+__device__ inline Cum4 wave_cum4(const double (&x)[4]) {
+    Cum4 r;
+    r.c[0] = x[0];
+    r.c[1] = r.c[0] + x[1];
+    r.c[2] = r.c[1] + x[2];
+    r.c[3] = r.c[2] + x[3];
+    const double incl = wave_incl_scan_f64(r.c[3]);
+    const double excl = incl - r.c[3];
+    for (int j = 0; j < 4; j++) r.c[j] += excl;
+    return r;
+}
+// The first element whose predicate holds (kNone when none).
+__device__ inline int wave_first4(const bool (&pred)[4]) {
+    int fj = 4;
+    for (int j = 3; j >= 0; j--) fj = pred[j] ? j : fj;
+    const uint64_t m = ballot(fj < 4);
+    if (!m) return kNone;
+    const int l = (int) __builtin_ctzll(m);
+    return 4 * l + __builtin_amdgcn_readlane(fj, l);
+}
+__device__ inline double wave_sum4(const double (&x)[4]) { return wave_sum_f64((x[0] + x[1]) + (x[2] + x[3])); }
+
+// Finishes a row from its totals and its n sorted top entries e[0..n), n <= kFinishMax, in one wave (the caller's
+// wave 0). Returns true when the row is done, false when it needs the multi-pass path (its top-p set or its draw
+// runs beyond the entries held). pf: LDS scratch of kFinishMax floats.
+__device__ inline bool finish_wave(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+                                   const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf) {
+    const int lane = lane_id();
     const double u = a.u ? a.u[row] : 0.0;
     const float top = n > 0 ? entry_value(e[0]) : -INFINITY;
     const int st = row_status(pl, p, tot.flags, n > 0 && __builtin_isfinite(top));
     if (st >= 0) {
-        if (tid == 0) write_row(a, row, -1, st, 0);
+        if (lane == 0) write_row(a, row, -1, st, 0);
         return true;
     }
     if (pl.mode == kGreedy) {
         // std::max_element: the first largest, or token 0 when its logit is NaN.
         const int id = ((tot.flags & kNaN0) || tot.best == 0) ? 0 : (int) entry_id(tot.best);
-        if (tid == 0) {
-            write_row(a, row, id, SPX_ROW_OK, 1);
-            if (a.out_cand_ids) {
-                for (int j = 0; j < a.max_out; j++) {
-                    a.out_cand_ids[(int64_t) row * a.max_out + j] = j == 0 ? id : -1;
-                    a.out_cand_probs[(int64_t) row * a.max_out + j] = j == 0 ? 1.0f : 0.0f;
-                }
+        if (lane == 0) write_row(a, row, id, SPX_ROW_OK, 1);
+        if (a.out_cand_ids) {
+            for (int j = lane; j < a.max_out; j += kWave) {
+                a.out_cand_ids[(int64_t) row * a.max_out + j] = j == 0 ? id : -1;
+                a.out_cand_probs[(int64_t) row * a.max_out + j] = j == 0 ? 1.0f : 0.0f;
             }
         }
         return true;
@@ -964,28 +897,38 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
     // Every candidate of the reference with a weight is held: its top k, or every token that has a key (the rest of
     // a short row are banned tokens, last in the order with weight 0).
     const bool full_known = nk >= pl.k || complete;
-    // the k-th candidate itself is held (it is not a banned token beyond the entries)
-    const bool last_held = nk >= pl.k;
-    const bool valid = tid < nk;
-    const float vi = valid ? entry_value(e[tid]) : -INFINITY;
-    // The sum of exp over the whole vocabulary, relative to the top value (m of the totals is that value or below).
-    const double s_all = pl.need_s ? tot.s * exp((double) tot.m - (double) top) : 0.0;
-    int kept = 0, pick = -1;
-    bool resolved = true;
+    const bool last_held = nk >= pl.k;  // the k-th candidate itself is held
     // Transformers and Haru normalize over their top k; beyond the entries held, only a top k of the whole
     // vocabulary has a known sum (the stream's). Other rows take the multi-pass path.
     if (!full_known && pl.k < a.vocab && pl.flavor != SPX_FLAVOR_FISH) return false;
+    // The sum of exp over the whole vocabulary, relative to the top value (m of the totals is that value or below).
+    const double s_all = pl.need_s ? tot.s * exp((double) tot.m - (double) top) : 0.0;
+    bool valid[4];
+    float v[4];
+    int idx[4];
+    for (int j = 0; j < 4; j++) {
+        idx[j] = 4 * lane + j;
+        valid[j] = idx[j] < nk;
+        v[j] = valid[j] ? entry_value(e[idx[j]]) : -INFINITY;
+    }
+    int kept = 0, pick = -1;
+    bool resolved = true;
+    double outp[4] = {0.0, 0.0, 0.0, 0.0};  // the candidates' reported weights
+    int nout = 0;                           // reported candidates
 
     if (pl.flavor == SPX_FLAVOR_TRANSFORMERS) {
         // candidates(): double softmax over the k kept, normalized by their sum (src/families/qwen3-tts/sampler.cpp:84-87)
-        const double w = valid ? exp((double) vi - (double) top) : 0.0;
-        const double sum = full_known ? block_sum_f64<B>(w, L.red) : s_all;
-        const double q = w / sum;
+        double w[4], q[4];
+        for (int j = 0; j < 4; j++) w[j] = valid[j] ? exp((double) v[j] - (double) top) : 0.0;
+        const double sum = full_known ? wave_sum4(w) : s_all;
+        for (int j = 0; j < 4; j++) q[j] = w[j] / sum;
         int keep = -1;
         if (pl.top_p < 1.0f) {
             // the smallest prefix whose cumulative weight reaches top_p, at least one (:88-99)
-            const double c = block_incl_scan_f64<B>(q, L.red);
-            const int first = block_min_i32<B>(valid && c >= (double) pl.top_p ? tid : kNone, L.ired);
+            const Cum4 c = wave_cum4(q);
+            bool pr[4];
+            for (int j = 0; j < 4; j++) pr[j] = valid[j] && c.c[j] >= (double) pl.top_p;
+            const int first = wave_first4(pr);
             if (first != kNone) keep = first + 1;
             else if (full_known) keep = nk;
             else resolved = false;
@@ -994,15 +937,15 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
         } else {
             // A draw over every token: pick()'s running share must pass u within the entries held. The shares are
             // the weights over the whole vocabulary's sum, which is what pick() divides by, to rounding.
-            const double c = block_incl_scan_f64<B>(q, L.red);
-            const int first = block_min_i32<B>(valid && c > u ? tid : kNone, L.ired);
+            const Cum4 c = wave_cum4(q);
+            bool pr[4];
+            for (int j = 0; j < 4; j++) pr[j] = valid[j] && c.c[j] > u;
+            const int first = wave_first4(pr);
             if (first != kNone && first < pl.k - 1) {
                 pick = first;
                 kept = pl.k;
-                if (a.out_cand_ids && valid && tid < a.max_out) {
-                    a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
-                    a.out_cand_probs[(int64_t) row * a.max_out + tid] = (float) q;
-                }
+                for (int j = 0; j < 4; j++) outp[j] = q[j];
+                nout = nk;
             } else {
                 resolved = false;
             }
@@ -1012,113 +955,137 @@ __device__ inline bool finish_row(const Launch & a, int row, const spx_row_param
             // k have a key (banned ones, weight 0, are the rest of the k), the last held is not pick()'s last.
             const bool short_k = pl.top_p >= 1.0f && !last_held;
             const int lim = short_k ? keep : keep - 1;
-            const bool in = tid < keep;
-            const double kq = in ? q : 0.0;
-            const double ksum = block_sum_f64<B>(kq, L.red);
-            const double c = block_incl_scan_f64<B>(in ? kq / ksum : 0.0, L.red);
-            const int first = block_min_i32<B>(in && tid < lim && c > u ? tid : kNone, L.ired);
+            double kq[4];
+            for (int j = 0; j < 4; j++) kq[j] = idx[j] < keep ? q[j] : 0.0;
+            const double ksum = wave_sum4(kq);
+            for (int j = 0; j < 4; j++) kq[j] /= ksum;
+            const Cum4 c = wave_cum4(kq);
+            bool pr[4];
+            for (int j = 0; j < 4; j++) pr[j] = idx[j] < lim && c.c[j] > u;
+            const int first = wave_first4(pr);
             if (first != kNone) pick = first;
             else if (!short_k) pick = keep - 1;
             else resolved = false;
             kept = short_k ? pl.k : keep;
-            if (a.out_cand_ids && in && tid < a.max_out) {
-                a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
-                a.out_cand_probs[(int64_t) row * a.max_out + tid] = (float) (kq / ksum);
-            }
+            for (int j = 0; j < 4; j++) outp[j] = kq[j];
+            nout = keep;
         }
     } else if (pl.flavor == SPX_FLAVOR_HARU) {
-        // torch's float32 softmax over the k kept and its top-p zeroing (src/families/haru/sampler.cpp:44-59)
-        if (valid) L.pf[tid] = (float) exp((double) (vi - top));
-        __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
+        // torch's float32 softmax over the k kept and its top-p zeroing (src/families/haru/sampler.cpp:44-59), the
+        // float sums in the reference's order by one lane
+        for (int j = 0; j < 4; j++)
+            if (valid[j]) pf[idx[j]] = (float) exp((double) (v[j] - top));
+        __builtin_amdgcn_wave_barrier();  // lane 0 reads what the wave wrote (LDS keeps one wave's order)
+        float sumf = 0.0f;
+        int zeros = 0;
+        if (lane == 0) {
             if (full_known) {
-                for (int i = 0; i < nk; i++) sum += L.pf[i];
+                for (int i = 0; i < nk; i++) sumf += pf[i];
             } else {
-                sum = (float) s_all;
+                sumf = (float) s_all;
             }
-            L.red[0] = (double) sum;
-        }
-        __syncthreads();
-        const float sumf = (float) L.red[0];
-        __syncthreads();
-        if (valid) L.pf[tid] = L.pf[tid] / sumf;
-        __syncthreads();
-        // The zeroing, position by position as the reference's loop runs it, in float (:52-59).
-        if (pl.top_p > 0.0f && pl.top_p < 1.0f) {
-            if (tid == 0) {
+            if (pl.top_p > 0.0f && pl.top_p < 1.0f) {
+                // The zeroing, position by position as the reference's loop runs it, in float (:52-59); pf[i] keeps
+                // p_i, or -p_i where it is zeroed.
                 float run = 0.0f;
-                int zeros = 0;
                 for (int i = 0; i < nk; i++) {
-                    const float pi = L.pf[i];
+                    const float pi = pf[i] / sumf;
                     run += pi;
                     const bool zero = !(run - pi < pl.top_p);
-                    L.w[i] = zero ? 0.0 : (double) pi;
                     zeros += zero ? 1 : 0;
+                    pf[i] = zero ? -pi : pi;
                 }
-                L.ired[48] = zeros;
+            } else {
+                for (int i = 0; i < nk; i++) pf[i] = pf[i] / sumf;
             }
-        } else if (tid == 0) {
-            for (int i = 0; i < nk; i++) L.w[i] = (double) L.pf[i];
-            L.ired[48] = 0;
         }
-        __syncthreads();
+        zeros = __builtin_amdgcn_readfirstlane(zeros);
         // Beyond the entries held the weights must be 0: a zero among them, the cumulative share only rising.
-        if (!full_known && L.ired[48] == 0) resolved = false;
-        const double w = valid ? L.w[tid] : 0.0;
-        __syncthreads();
+        if (!full_known && zeros == 0) resolved = false;
         if (resolved) {
+            double w[4];
+            for (int j = 0; j < 4; j++) {
+                const float x = valid[j] ? pf[idx[j]] : 0.0f;
+                w[j] = x > 0.0f ? (double) x : 0.0;
+            }
+            const double ksum = wave_sum4(w);
+            for (int j = 0; j < 4; j++) w[j] /= ksum;
             // pick() over all k weights, zeros included: the held k-th is its last; short of it, its last lies beyond
             const int lim = last_held ? nk - 1 : nk;
-            const double ksum = block_sum_f64<B>(w, L.red);
-            const double c = block_incl_scan_f64<B>(w / ksum, L.red);
-            const int first = block_min_i32<B>(valid && tid < lim && c > u ? tid : kNone, L.ired);
+            const Cum4 c = wave_cum4(w);
+            bool pr[4];
+            for (int j = 0; j < 4; j++) pr[j] = valid[j] && idx[j] < lim && c.c[j] > u;
+            const int first = wave_first4(pr);
             if (first != kNone) pick = first;
             else if (last_held) pick = nk - 1;
             else resolved = false;
             kept = pl.k;
-            if (a.out_cand_ids && valid && tid < a.max_out) {
-                a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
-                a.out_cand_probs[(int64_t) row * a.max_out + tid] = (float) (w / ksum);
-            }
+            for (int j = 0; j < 4; j++) outp[j] = w[j];
+            nout = nk;
         }
     } else {
         // fish-speech: shares over the softmax of every logit, the token passing top_p dropped
         // (src/families/drama3/sampler.cpp:48-59)
-        const double w = valid ? exp((double) vi - (double) top) : 0.0;
-        const double c = block_incl_scan_f64<B>(w / s_all, L.red);
-        const int first = block_min_i32<B>(valid && tid > 0 && c > (double) pl.top_p ? tid : kNone, L.ired);
-        int keep;
+        double w[4], sh[4];
+        for (int j = 0; j < 4; j++) {
+            w[j] = valid[j] ? exp((double) v[j] - (double) top) : 0.0;
+            sh[j] = w[j] / s_all;
+        }
+        const Cum4 c = wave_cum4(sh);
+        bool pr[4];
+        for (int j = 0; j < 4; j++) pr[j] = valid[j] && idx[j] > 0 && c.c[j] > (double) pl.top_p;
+        const int first = wave_first4(pr);
+        int keep = -1;
         if (first != kNone) keep = first;
         else if (full_known) keep = nk;
-        else {
-            keep = -1;
-            resolved = false;
-        }
+        else resolved = false;
         if (resolved) {
-            const bool in = tid < keep;
-            const double kw = in ? w : 0.0;
-            const double ksum = block_sum_f64<B>(kw, L.red);
-            const double cc = block_incl_scan_f64<B>(kw / ksum, L.red);
-            const int f2 = block_min_i32<B>(in && tid < keep - 1 && cc > u ? tid : kNone, L.ired);
+            double kw[4];
+            for (int j = 0; j < 4; j++) kw[j] = idx[j] < keep ? w[j] : 0.0;
+            const double ksum = wave_sum4(kw);
+            for (int j = 0; j < 4; j++) kw[j] /= ksum;
+            const Cum4 cc = wave_cum4(kw);
+            bool pr2[4];
+            for (int j = 0; j < 4; j++) pr2[j] = idx[j] < keep - 1 && cc.c[j] > u;
+            const int f2 = wave_first4(pr2);
             pick = f2 != kNone ? f2 : keep - 1;
             kept = keep;
-            if (a.out_cand_ids && in && tid < a.max_out) {
-                a.out_cand_ids[(int64_t) row * a.max_out + tid] = (int32_t) entry_id(e[tid]);
-                a.out_cand_probs[(int64_t) row * a.max_out + tid] = (float) (kw / ksum);
-            }
+            for (int j = 0; j < 4; j++) outp[j] = kw[j];
+            nout = keep;
         }
     }
     if (!resolved) return false;
-    if (tid == 0) write_row(a, row, (int) entry_id(e[pick]), SPX_ROW_OK, kept);
+    if (lane == 0) write_row(a, row, (int) entry_id(e[pick]), SPX_ROW_OK, kept);
     if (a.out_cand_ids) {
+        for (int j = 0; j < 4; j++) {
+            const int i = idx[j];
+            if (i < nout && i < a.max_out) {
+                a.out_cand_ids[(int64_t) row * a.max_out + i] = (int32_t) entry_id(e[i]);
+                a.out_cand_probs[(int64_t) row * a.max_out + i] = (float) outp[j];
+            }
+        }
         // entries past those written above
-        for (int j = min(kept, nk) + tid; j < a.max_out; j += B) {
-            a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
-            a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
+        for (int j = min(kept, nk) + lane; j < a.max_out; j += kWave) {
+            if (j >= nout) {
+                a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
+                a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
+            }
         }
     }
     return true;
+}
+
+// Wave 0 finishes the row; the work-group learns whether it must take the multi-pass path.
+template <int B>
+__device__ inline bool finish_block(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+                                    const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf,
+                                    Ctl * ctl) {
+    if (threadIdx.x < kWave) {
+        const bool ok = finish_wave(a, row, p, pl, tot, e, min(n, kFinishMax), complete, pf);
+        if (threadIdx.x == 0) ctl->resolved = ok ? 1u : 0u;
+    }
+    __syncthreads();
+    return ctl->resolved != 0;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1418,22 +1385,25 @@ __device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & sp
     split = g - row * splits;
 }
 
-// Counts this chunk in after its partial is published; true in the row's last chunk, whose threads then see every
-// partial of the row.
+// Counts this chunk in after wave 0 has written its partial: a release at agent scope by that wave (the L2 of this
+// XCD written back), one atomic per chunk; true in the row's last chunk, whose acquire (its caches invalidated) lets
+// every thread then read the other chunks' partials. The other waves take no fence.
 template <int B>
 __device__ inline bool arrive_last(const Launch & a, int row, Ctl * ctl) {
-    __threadfence();  // this thread's part of the partial is visible device-wide
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned prev = atomicAdd(&a.counters[row], 1u);
-        const bool last = prev == (unsigned) (a.splits - 1);
-        if (last) a.counters[row] = 0;  // ready for the next launch
-        ctl->last = last ? 1u : 0u;
+    if (threadIdx.x < kWave) {
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+        if (threadIdx.x == 0) {
+            const unsigned prev = __hip_atomic_fetch_add(&a.counters[row], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const bool last = prev == (unsigned) (a.splits - 1);
+            if (last) {
+                a.counters[row] = 0;  // ready for the next launch
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+            }
+            ctl->last = last ? 1u : 0u;
+        }
     }
     __syncthreads();
-    const bool last = ctl->last != 0;
-    if (last) __threadfence();  // the other chunks' partials are read after this
-    return last;
+    return ctl->last != 0;
 }
 
 // Token 0's final logit, where it is not a history token, for std::max_element's NaN in front.
@@ -1445,10 +1415,59 @@ __device__ inline uint32_t nan0_flag(const T * rowp, const Plan & pl, const Spec
     return __builtin_isnan(load_one<T>(rowp)) ? kNaN0 : 0u;
 }
 
+// Appends the entries of src[0..n) at or above `floor` to dst (at most kSortCap), one wave at a time per 64: a ballot,
+// one atomic per wave on the LDS count, no barrier. The order among the appended is free; the caller sorts.
+template <int B>
+__device__ inline void gather_append(const uint64_t * src, int n, uint64_t floor, uint64_t * dst, uint32_t * count) {
+    const int lane = lane_id();
+    for (int i0 = (threadIdx.x / kWave) * kWave; i0 < n; i0 += B) {
+        const int i = i0 + lane;
+        const uint64_t e = i < n ? src[i] : 0ull;
+        const bool keep = e != 0 && e >= floor;
+        const uint64_t m = ballot(keep);
+        if (!m) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(count, (uint32_t) __popcll(m));
+        base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
+        const uint32_t pos = base + (uint32_t) lanes_below(m);
+        if (keep && pos < (uint32_t) kSortCap) dst[pos] = e;
+    }
+}
+
+// Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
+// their ids differ), reading the list as LDS broadcasts, two entries per read.
+template <int B>
+__device__ inline void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
+    for (int i = threadIdx.x; i < n; i += B) {
+        const uint64_t e = src[i];
+        int r = 0;
+        int j = 0;
+        for (; j + 1 < n; j += 2) {
+            r += src[j] > e ? 1 : 0;
+            r += src[j + 1] > e ? 1 : 0;
+        }
+        if (j < n) r += src[j] > e ? 1 : 0;
+        dst[r] = e;
+    }
+    __syncthreads();
+}
+
+// The chunk's candidates at or above `floor`, gathered from buf[0..nb) and sorted into dst; returns how many there
+// are (beyond kSortCap only the count is exact).
+template <int B>
+__device__ inline int gather_sort(const uint64_t * buf, int nb, uint64_t floor, uint64_t * tmp, uint64_t * dst,
+                                  uint32_t * count) {
+    gather_append<B>(buf, nb, floor, tmp, count);
+    __syncthreads();
+    const int total = (int) *count;
+    rank_sort<B>(tmp, min(total, kSortCap), dst);
+    return total;
+}
+
 template <typename T, int B>
 __device__ inline void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
-                                  uint32_t bad, unsigned char * lds) {
+                                  uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V;
     constexpr int W = B / kWave;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
@@ -1463,17 +1482,54 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     st.m = -INFINITY;
     st.hi = -FLT_MAX;
     st.tau = -INFINITY;
-    st.lo = 0.0f;
-    st.inv = 0.0f;
-    st.delta = 0.0f;
-    st.hist_on = 0;
     st.flags = 0;
     GreedySt g;
     StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, cand, cap};
-    if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1);
-    else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1);
+    if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1, first);
+    else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1, first);
 
-    // The stream's totals: each wave's sum relative to its m, corrected for the rounding of m*L; then the chunk's.
+    // The history tokens (penalties, the ban), one per thread, with the statistics and the threshold of the stream:
+    // a term against the wave's reference (raised first where a quotient passes it), the flags, an entry.
+    if (pl.pen && sp.n_slots > 0) {
+        __syncthreads();  // the captures and the stream's appends are done
+        const int npairs = sp.n_slots * V;
+        const uint32_t tk = ctl->tau_key;
+        const float tau = tk ? key_float(tk) : -INFINITY;
+        for (int i0 = 0; i0 < npairs; i0 += B) {
+            const int i = i0 + tid;
+            HistTok h;
+            const bool ok = i < npairs && hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h);
+            const bool live = ok && !h.banned;
+            float q = -INFINITY;
+            if (ok && h.id == 0 && __builtin_isnan(h.v)) st.flags |= kNaN0;
+            if (live) {
+                q = div_rn(h.v, pl.t, pl.rt);
+                if (__builtin_isnan(h.v)) st.flags |= kNaN;
+                else if (h.v == INFINITY) st.flags |= kPosInf;
+                else if (h.v == -INFINITY) st.flags |= kNegInf;
+                else {
+                    st.flags |= kFinite;
+                    if (!__builtin_isfinite(q)) st.flags |= kTempOver;
+                }
+            }
+            const bool fin = live && q > -INFINITY && q < INFINITY;
+            const float wm = uniform_f(wave_max_f32(fin ? q : -INFINITY));
+            if (wm > st.m) {
+                const float nhi = wm * kL2e;
+                if (st.m > -INFINITY) st.s *= exp2((double) st.hi - (double) nhi);
+                st.m = wm;
+                st.hi = nhi;
+            }
+            if (fin) st.s += (double) __builtin_amdgcn_exp2f(__builtin_fmaf(q, kL2e, -st.hi));
+            if (live && !__builtin_isnan(q) && q >= tau) {
+                const uint32_t pos = atomicAdd(&ctl->n, 1u);
+                if (pos < (uint32_t) cap) cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
+                else ctl->overflow = 1u;
+            }
+        }
+    }
+
+    // The chunk's totals: each wave's sum relative to its m, corrected for the rounding of m*L, then the waves'.
     {
         double ws = wave_sum_f64(st.s);
         if (st.m > -INFINITY) ws *= exp2(-(double) __builtin_fmaf(st.m, kL2e, -st.hi));
@@ -1485,6 +1541,7 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
             red->f[wave] = st.m;
             red->w[wave] = wf | f0;
         }
+        if (tid == 0) ctl->ncomp = 0;
     }
     __syncthreads();
     float M = -INFINITY;
@@ -1496,93 +1553,36 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     double S = 0.0;
     for (int w = 0; w < W; w++)
         if (red->f[w] > -INFINITY) S += red->d[w] * exp((double) red->f[w] - (double) M);
-    __syncthreads();
-
-    // The history tokens: penalties, the ban, then the same statistics and the same threshold.
-    if (pl.pen && sp.n_slots > 0) {
-        const int npairs = sp.n_slots * V;
-        float hm = -INFINITY;
-        uint32_t hf = 0;
-        for (int i = tid; i < npairs; i += B) {
-            HistTok h;
-            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h)) continue;
-            if (h.id == 0 && __builtin_isnan(h.v)) hf |= kNaN0;
-            if (h.banned) continue;
-            const float q = div_rn(h.v, pl.t, pl.rt);
-            if (__builtin_isnan(h.v)) hf |= kNaN;
-            else if (h.v == INFINITY) hf |= kPosInf;
-            else if (h.v == -INFINITY) hf |= kNegInf;
-            else {
-                hf |= kFinite;
-                if (!__builtin_isfinite(q)) hf |= kTempOver;
-            }
-            if (q > -INFINITY && q < INFINITY) hm = fmaxf(hm, q);
-        }
-        hm = block_max_f32<B>(hm, red->f);
-        F |= block_or_u32<B>(hf, red->w);
-        if (hm > M) {
-            if (M > -INFINITY) S *= exp((double) M - (double) hm);
-            M = hm;
-        }
-        const uint32_t tk = ctl->tau_key;
-        const float tau = tk ? key_float(tk) : -INFINITY;
-        double hs = 0.0;
-        for (int i = tid; i < npairs; i += B) {
-            HistTok h;
-            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h) || h.banned) continue;
-            const float q = div_rn(h.v, pl.t, pl.rt);
-            if (q > -INFINITY && q < INFINITY) hs += exp((double) q - (double) M);
-            if (!__builtin_isnan(q) && q >= tau) {
-                const uint32_t pos = atomicAdd(&ctl->n, 1u);
-                if (pos < (uint32_t) cap) cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
-                else ctl->overflow = 1u;
-            }
-        }
-        S += block_sum_f64<B>(hs, red->d);
-    }
     // A finite quotient has a term above 0 against the largest one: S > 0. Every logit that is not finite, and every
     // finite one whose quotient is not (the correction step gives NaN for both), went through the exact path, which
     // set the flags.
     if (S > 0.0) F |= kFinite;
 
-    // The candidates at or above the final threshold, sorted.
-    __syncthreads();
+    // The candidates at or above the final threshold, gathered, then sorted by rank.
     const uint32_t nres = ctl->n;
     const bool overflow = ctl->overflow != 0 || nres > (uint32_t) cap;
     const int nb = min((int) nres, cap);
     const uint32_t tkey = ctl->tau_key;
-    const uint64_t floor = (uint64_t) tkey << 32;
     const bool complete = tkey <= order_key(-INFINITY) && !overflow;  // the threshold never left -inf
-    int total = 0;
-    for (int i0 = 0; i0 < nb; i0 += B) {
-        const int i = i0 + tid;
-        const uint64_t e = i < nb ? cand[i] : 0ull;
-        const bool keep = e != 0 && e >= floor;
-        int cnt;
-        const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, red->i, cnt);
-        if (keep && total + pos < kSortCap) sorted[total + pos] = e;
-        total += cnt;
+    // The chunk's K-th key, by wave 0: every token at or above it is in the buffer (it is at or above every
+    // threshold the stream had), and at least K entries are.
+    if (!complete && tid < kWave) {
+        const uint32_t kk = buffer_bound(cand, nb, pl.K);
+        if (tid == 0) ctl->kkey = kk;
     }
+    __syncthreads();
+    const uint32_t kk = ctl->kkey;
+    const uint32_t fkey = complete ? tkey : (kk > tkey ? kk : tkey);
+    const uint64_t floor = (uint64_t) fkey << 32;
+    const int total = gather_sort<B>(cand, nb, floor, sorted, cand, &ctl->ncomp);
     const bool too_many = total > kSortCap;
-    total = min(total, kSortCap);
-    {
-        int np2 = 1;
-        while (np2 < total) np2 <<= 1;
-        for (int i = total + tid; i < np2; i += B) sorted[i] = 0;
-        __syncthreads();
-        block_sort_desc<B>(sorted, np2);
-    }
     const bool broken = overflow || too_many;
-
-    FinishLds L;
-    L.w = (double *) cand;
-    L.red = red->d;
-    L.ired = red->i;
-    L.pf = (float *) (cand + B);
+    const int ntot = min(total, kSortCap);
+    float * pf = (float *) sorted;  // the gathered copy is read no more
 
     if (a.splits == 1) {
         RowTotals t{0ull, S, M, F};
-        if (broken || !finish_row<B>(a, row, p, pl, t, sorted, min(total, B), complete, L)) {
+        if (broken || !finish_block<B>(a, row, p, pl, t, cand, ntot, complete, pf, ctl)) {
             __syncthreads();
             fallback_row<T, B>(a, row, p, pl, F, lds);
         }
@@ -1592,16 +1592,18 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     // Publish this chunk's partial; the last chunk of the row to arrive merges them.
     Partial * part = a.partials + (int64_t) row * a.splits + split;
     uint64_t * pc = a.part_cands + ((int64_t) row * a.splits + split) * kKeep;
-    const int npub = min(total, kKeep);
-    for (int i = tid; i < npub; i += B) pc[i] = sorted[i];
+    const int npub = min(ntot, kKeep);
+    if (tid < kWave) {
+        for (int i = tid; i < npub; i += kWave) pc[i] = cand[i];
+    }
     if (tid == 0) {
         part->best = 0;
-        part->floor = total > kKeep ? sorted[kKeep - 1] : floor;
+        part->floor = ntot > kKeep ? cand[kKeep - 1] : floor;
         part->s = S;
         part->m = M;
         part->flags = F;
         part->n = npub;
-        part->complete = (complete && total <= kKeep) ? 1 : 0;
+        part->complete = (complete && ntot <= kKeep) ? 1 : 0;
         part->broken = broken ? 1 : 0;
     }
     if (!arrive_last<B>(a, row, ctl)) return;
@@ -1624,26 +1626,19 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     if (t.s > 0.0) t.flags |= kFinite;
     int tot = 0;
     if (!any_broken) {
+        // the chunks' entries at or above the highest floor, one chunk after the other, then sorted by rank
+        if (tid == 0) ctl->ncomp = 0;
+        __syncthreads();
         for (int s2 = 0; s2 < a.splits; s2++) {
             const int ns = pr[s2].n;
             const uint64_t * src = a.part_cands + ((int64_t) row * a.splits + s2) * kKeep;
-            for (int i0 = 0; i0 < ns; i0 += B) {
-                const int i = i0 + tid;
-                const bool keep = i < ns && src[i] >= fl;
-                int cnt;
-                const int pos = block_excl_scan_i32<B>(keep ? 1 : 0, red->i, cnt);
-                if (keep && tot + pos < kSortCap) sorted[tot + pos] = src[i];
-                tot += cnt;
-            }
+            gather_append<B>(src, ns, fl, sorted, &ctl->ncomp);
         }
-        tot = min(tot, kSortCap);
-        int np2 = 1;
-        while (np2 < tot) np2 <<= 1;
-        for (int i = tot + tid; i < np2; i += B) sorted[i] = 0;
         __syncthreads();
-        block_sort_desc<B>(sorted, np2);
+        tot = min((int) ctl->ncomp, kSortCap);
+        rank_sort<B>(sorted, tot, cand);
     }
-    if (any_broken || !finish_row<B>(a, row, p, pl, t, sorted, min(tot, B), all_complete, L)) {
+    if (any_broken || !finish_block<B>(a, row, p, pl, t, cand, tot, all_complete, pf, ctl)) {
         __syncthreads();
         fallback_row<T, B>(a, row, p, pl, t.flags, lds);
     }
@@ -1652,7 +1647,7 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
 template <typename T, int B>
 __device__ inline void greedy_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
-                                  uint32_t bad, unsigned char * lds) {
+                                  uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V;
     constexpr int W = B / kWave;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
@@ -1666,8 +1661,8 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
     g.nanb = 0;
     SampleSt st;
     StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, nullptr, 0};
-    if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1);
-    else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1);
+    if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1, first);
+    else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1, first);
 
     {
         const uint64_t be = g.bi >= 0 ? make_entry(order_key(g.bx), (uint32_t) g.bi) : 0ull;
@@ -1711,14 +1706,9 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
     }
     if (pl.xmin && xmin == -INFINITY) F |= kNegInf;
 
-    FinishLds L;
-    L.w = nullptr;
-    L.red = red->d;
-    L.ired = red->i;
-    L.pf = nullptr;
     if (a.splits == 1) {
         RowTotals t{best, 0.0, 0.0f, F | best_flags(best)};
-        finish_row<B>(a, row, p, pl, t, nullptr, 0, true, L);
+        if (tid < kWave) finish_wave(a, row, p, pl, t, nullptr, 0, true, nullptr);
         return;
     }
     Partial * part = a.partials + (int64_t) row * a.splits + split;
@@ -1737,7 +1727,7 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
         t.flags |= q.flags;
     }
     t.flags |= best_flags(t.best);
-    finish_row<B>(a, row, p, pl, t, nullptr, 0, true, L);
+    if (tid < kWave) finish_wave(a, row, p, pl, t, nullptr, 0, true, nullptr);
 }
 
 template <typename T, int B>
@@ -1781,11 +1771,13 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
         ctl->overflow = 0;
         ctl->last = 0;
     }
-    if (tid < kBuckets) ctl->hist[tid] = 0;
     if (sampling) {
         uint64_t * cand = (uint64_t *) (lds + a.off_cand);
         for (int i = tid; i < a.cand_cap; i += B) cand[i] = 0;
     }
+    // The first step's logits are on their way while the special tokens are built.
+    U32x4 first[Elt<T>::U];
+    load_first<T, B>(a, rowp, c0, c1, first);
     Specials sp;
     sp.spec = (uint2 *) (lds + a.off_spec);
     sp.meta = (uint32_t *) (lds + a.off_meta);
@@ -1797,8 +1789,8 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     uint32_t bad = 0;
     if (sp.any) build_specials<B, V>(sp, a, row, c0, c1, pl, banned_row, red->i, bad);
     __syncthreads();
-    if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds);
-    else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds);
+    if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
+    else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
