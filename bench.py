@@ -9,6 +9,9 @@ bytes per launch over its average launch time, from HIP events recorded on the l
 the oracle (a C++ restatement of the reference's sampler) timed on a bounded sample of the same rows on this host.
 
 usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload haru] [--cpu-rows 48] [--no-cpu]
+       python bench.py --copy-mb 512 [--steps 20]   a plain device-to-device copy of known size (calibrates the
+                                                   FETCH_SIZE / WRITE_SIZE counters)
+       python bench.py --pmc-summary counter_collection.csv   per-kernel dispatch averages of a rocprofv3 --pmc run
 """
 
 import argparse
@@ -42,7 +45,42 @@ def parse():
     ap.add_argument("--cpu-rows", type=int, default=48)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--seed", type=int, default=1234)
+    ap.add_argument("--copy-mb", type=int, default=0)
+    ap.add_argument("--pmc-summary", default=None)
     return ap.parse_args()
+
+
+def copy_calibration(mb, steps, warmup):
+    """`steps` copies of `mb` MiB from one HBM buffer to another: a kernel whose traffic is known exactly (mb MiB
+    read, mb MiB written per dispatch), which scales what FETCH_SIZE and WRITE_SIZE report for the sampler."""
+    import torch
+    n = (mb << 20) // 4
+    src = torch.arange(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    for _ in range(steps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_mib": mb, "bytes_read_per_dispatch": mb << 20, "bytes_written_per_dispatch": mb << 20,
+                      "steps": steps}))
+
+
+def pmc_summary(path):
+    """Average of every counter column of a rocprofv3 counter_collection.csv, per kernel name."""
+    import csv
+    acc = {}
+    with open(path) as f:
+        for r in csv.DictReader(f):
+            name = r.get("Kernel_Name", "?")
+            key = (name, r.get("Counter_Name", "?"))
+            v = float(r.get("Counter_Value", "nan"))
+            a = acc.setdefault(key, [0.0, 0])
+            a[0] += v
+            a[1] += 1
+    for (name, ctr), (tot, n) in sorted(acc.items()):
+        print(json.dumps({"kernel": name, "counter": ctr, "dispatches": n, "mean_per_dispatch": tot / n}))
 
 
 def cpu_baseline(w, rows, threads_list):
@@ -90,11 +128,17 @@ def cpu_model():
 
 def main():
     args = parse()
+    if args.pmc_summary:
+        pmc_summary(args.pmc_summary)
+        return
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "rows shard across GPUs with no exchange, so the N-GPU rate is N times the one-GPU rate.",
               file=sys.stderr)
         sys.exit(2)
+    if args.copy_mb:
+        copy_calibration(args.copy_mb, args.steps, args.warmup)
+        return
     import torch
     import gpu_harness
     import workloads
