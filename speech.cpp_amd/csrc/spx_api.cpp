@@ -42,7 +42,7 @@ size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool ha
     using namespace spx;
     size_t off = 0;
     a.off_ctl = (int) off;
-    off += 1024;
+    off += kCtlBytes;
     a.off_red = (int) off;
     off += 1280;
     const size_t words = (size_t) (chunk + 31) / 32;

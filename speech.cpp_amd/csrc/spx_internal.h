@@ -23,6 +23,8 @@ constexpr int kKeepFull = 128;
 constexpr int kSortCap = 1024;
 constexpr int kMaxSplits = 4;
 constexpr int kMaxSplitsGreedy = 16;
+// LDS bytes of a chunk's control block (its counters, bins and first-step bounds).
+constexpr int kCtlBytes = 2048;
 // The largest history a handle takes: slot ranks are kept in 24 bits and the LDS must hold the slots.
 constexpr int kMaxHist = 4096;
 

@@ -202,7 +202,10 @@ __device__ inline uint64_t block_min_u64(uint64_t v, uint64_t * red) {
 }
 
 // The control block of a chunk, in LDS.
+constexpr int kBins = 256;
+
 struct Ctl {
+    uint32_t bins[kBins];  // candidate entries per bin of quotient (sampling rows, from the first step on)
     uint32_t n;         // candidate entries reserved
     uint32_t tau_key;   // order key of the threshold (0: none yet)
     uint32_t overflow;  // entries were dropped for want of room
@@ -210,9 +213,14 @@ struct Ctl {
     uint32_t resolved;  // the finishing wave settled the row
     uint32_t ncomp;     // candidates at or above the final threshold
     uint32_t kkey;      // the chunk's K-th key
+    // The bins of the candidates' quotients, set by the first step: bin (q - lo) * scale clamped to [0, kBins), a
+    // bin `width` about 1 / scale wide; scale 0: no bins (the first step gave no finite bound), the threshold moves
+    // by exact searches. Kept here rather than in registers: they are read where a candidate is appended.
+    float bin_lo, bin_scale, bin_width;
     float wave_t[16];   // per wave: its bound on the K-th quotient, and its largest quotient, of the first step
     float wave_m[16];
 };
+static_assert(sizeof(Ctl) <= kCtlBytes, "the control block outgrows its LDS");
 
 // ------------------------------------------------------------------------------------------------------------------
 // Special tokens of a chunk, in LDS
@@ -254,24 +262,44 @@ __device__ inline uint32_t vec_mask(uint32_t h) {
     return m;
 }
 
+// History ids each thread holds: thread t the row's ids t, t + B, ... (a history is at most kMaxHist ids).
+template <int B>
+struct HistIds {
+    static constexpr int R = kMaxHist / B;
+    int id[R];
+};
+
+// The row's history ids, requested ahead of the first step's logits (-1 past the row's history).
+template <int B>
+__device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan & pl, HistIds<B> & h, uint32_t & bad) {
+#pragma unroll
+    for (int r = 0; r < HistIds<B>::R; r++) h.id[r] = -1;
+    if (!pl.pen) return;
+    const int h0 = a.hist_off[row];
+    int h1 = a.hist_off[row + 1];
+    if (h1 - h0 > a.max_hist || h1 < h0) {
+        bad |= kBadHist;
+        h1 = h0;
+    }
+#pragma unroll
+    for (int r = 0; r < HistIds<B>::R; r++) {
+        const int j = h0 + (int) threadIdx.x + r * B;
+        if (j < h1) h.id[r] = a.hist[j];
+    }
+}
+
 template <int B, int V>
 __device__ inline void build_specials(Specials & sp, const Launch & a, int row, int c0, int c1, const Plan & pl,
-                                      const uint32_t * banned_row, int * red, uint32_t & bad) {
+                                      const uint32_t * banned_row, int * red, const HistIds<B> & hist) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
     for (int w = tid; w < nw; w += B) sp.spec[w] = make_uint2(0u, 0u);
     __syncthreads();
-    int h0 = 0, h1 = 0;
     if (pl.pen) {
-        h0 = a.hist_off[row];
-        h1 = a.hist_off[row + 1];
-        if (h1 - h0 > a.max_hist || h1 < h0) {
-            bad |= kBadHist;
-            h1 = h0;
-        }
         // the history bits, in .y for now
-        for (int j = h0 + tid; j < h1; j += B) {
-            const int t = a.hist[j];
+#pragma unroll
+        for (int r = 0; r < HistIds<B>::R; r++) {
+            const int t = hist.id[r];
             if (t >= c0 && t < c1) atomicOr(&sp.spec[(t - c0) >> 5].y, 1u << ((t - c0) & 31));
         }
         __syncthreads();
@@ -316,8 +344,9 @@ __device__ inline void build_specials(Specials & sp, const Launch & a, int row, 
     if (pl.counts) {
         for (int s = tid; s < tu; s += B) sp.cnt[s] = 0;
         __syncthreads();
-        for (int j = h0 + tid; j < h1; j += B) {
-            const int t = a.hist[j];
+#pragma unroll
+        for (int r = 0; r < HistIds<B>::R; r++) {
+            const int t = hist.id[r];
             if (t >= c0 && t < c1) {
                 const int o = t - c0;
                 const uint32_t info = sp.spec[o >> 5].y;
@@ -383,10 +412,57 @@ __device__ inline bool hist_token(const Specials & sp, int i, int c0, const spx_
 
 struct SampleSt {
     double s;        // lane: sum of 2^(q*L - hi) over its groups, L = log2(e) in float
-    float m, hi;     // wave: the reference quotient and RN(m*L) (-FLT_MAX while no finite quotient is known)
+    float m, hi;     // wave: the reference quotient and ceil(m*L), an integer (-FLT_MAX while no finite quotient is known)
     float tau;       // wave: a quotient at or above it enters the buffer
     uint32_t flags;  // lane
 };
+
+// The largest float below a finite t (t itself when it is infinite).
+__device__ __forceinline__ float next_down(float t) {
+    const uint32_t u = __float_as_uint(t);
+    if (!(__builtin_fabsf(t) < INFINITY)) return t;
+    if (t == 0.0f) return -0x1p-149f;
+    return __uint_as_float(t > 0.0f ? u - 1u : u + 1u);
+}
+
+// The bin of a candidate's quotient (monotone in q).
+__device__ __forceinline__ int value_bin(float lo, float scale, float q) {
+    return (int) fminf(fmaxf((q - lo) * scale, 0.0f), (float) (kBins - 1));
+}
+
+// A threshold from the bins: the highest bin b whose bins b.. hold at least K candidates, and the threshold one bin
+// below it (every candidate of bins b.. is at or above it, whatever the rounding of the bin's computation); -inf
+// when fewer than K candidates are binned or b is the lowest bin. `held`: the candidates of bins b-1.. (about those
+// at or above the threshold). One wave; each lane reads four bins.
+__device__ __forceinline__ float bin_bound(const Ctl * ctl, int K, uint32_t & held) {
+    const int l = lane_id();
+    const uint4 c = ((const uint4 *) ctl->bins)[l];
+    const uint32_t s4 = c.x + c.y + c.z + c.w;
+    const uint32_t incl = (uint32_t) wave_incl_scan_i32((int) s4);
+    const uint32_t total = (uint32_t) __builtin_amdgcn_readlane((int) incl, kWave - 1);
+    held = 0;
+    // candidates in bins 4l+j and above
+    const uint32_t s3 = total - incl + c.w, s2 = s3 + c.z, s1 = s2 + c.y, s0 = s1 + c.x;
+    const uint64_t ok = ballot(s0 >= (uint32_t) K);
+    if (!ok) return -INFINITY;
+    const int top = kWave - 1 - (int) __builtin_clzll(ok);
+    const uint32_t uk = (uint32_t) K;
+    const int b = s3 >= uk ? 4 * l + 3 : s2 >= uk ? 4 * l + 2 : s1 >= uk ? 4 * l + 1 : 4 * l;
+    const int bb = __builtin_amdgcn_readlane(b, top);
+    if (bb < 1) return -INFINITY;
+    const int hb = bb - 1, hj = hb & 3;
+    held = (uint32_t) __builtin_amdgcn_readlane((int) (hj == 0 ? s0 : hj == 1 ? s1 : hj == 2 ? s2 : s3), hb >> 2);
+    // lo + (b-1) * width in one rounding, then one float down: below the exact edge
+    return next_down(__builtin_fmaf((float) (bb - 1), ctl->bin_width, ctl->bin_lo));
+}
+
+// The exponent the terms of a sum are taken against: an integer, so that moving a sum to a new one is exact.
+__device__ __forceinline__ float ref_exponent(float m) { return __builtin_ceilf(m * kL2e); }
+
+// A sum of 2^(q*L - hi) moved to the exponent nhi >= hi: a multiplication by a power of two.
+__device__ __forceinline__ double rescale(double s, float hi, float nhi) {
+    return __builtin_ldexp(s, (int) fmaxf(hi - nhi, -2000.0f));
+}
 
 // The first step: every wave bounds the K-th quotient by the kw-th largest of its lanes' maxima (each lane's maximum
 // is a distinct token), the work-group takes the smallest bound (kw lanes of every wave lie at or above it: at least
@@ -421,22 +497,40 @@ __device__ __forceinline__ void bootstrap(const Plan & pl, SampleSt & st, Ctl * 
     tau0 = uniform_f(tau0);
     mref = uniform_f(mref);
     st.tau = tau0;
+    float scale = 0.0f, width = 0.0f;
+    if (tau0 > -INFINITY && mref > tau0) {
+        const float span = mref - tau0;
+        const float sc = (float) kBins / span;
+        if (sc > 0.0f && sc < INFINITY && span < INFINITY) {
+            scale = sc;
+            width = span / (float) kBins;
+        }
+    }
+    // every wave writes the same values before it reads them
+    if (lane_id() == 0) {
+        __hip_atomic_store(&ctl->bin_lo, tau0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(&ctl->bin_scale, scale, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        __hip_atomic_store(&ctl->bin_width, width, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    }
+    __builtin_amdgcn_wave_barrier();
     st.m = mref;
-    st.hi = mref > -INFINITY ? mref * kL2e : -FLT_MAX;
+    st.hi = mref > -INFINITY ? ref_exponent(mref) : -FLT_MAX;
     if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tau0));
 }
 
 // A group with a term that is not a finite number below 2^100: exact quotients, the flags, a new reference m where a
-// finite quotient passes the old one, and the group's sum again.
-__device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE], const float (&x)[kE], uint32_t kill,
-                                  bool mask) {
+// finite quotient passes the old one, and the group's sum again. The logits are read again (element k is token
+// id_base + (k / VV) * B * VV + k % VV): the stream does not keep them past the quotients.
+template <typename T, int B, int VV>
+__device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE], const T * rowp, int id_base,
+                                  uint32_t kill, bool mask) {
     float gm = -INFINITY;
     uint32_t fl = 0;
 #pragma unroll
     for (int k = 0; k < kE; k++) {
         float qe = -INFINITY;
         if (!(mask && ((kill >> k) & 1u))) {
-            const float xv = x[k];
+            const float xv = load_one<T>(rowp + id_base + (k / VV) * (B * VV) + (k % VV));
             qe = div_rn(xv, pl.t, pl.rt);
             if (__builtin_isnan(qe)) fl |= kNaN;
             else if (qe == INFINITY) fl |= xv == INFINITY ? kPosInf : kTempOver;
@@ -449,8 +543,8 @@ __device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE]
     st.flags |= fl;
     const float wm = uniform_f(wave_max_f32(gm));
     if (wm > st.m) {
-        const float nhi = wm * kL2e;
-        if (st.m > -INFINITY) st.s *= exp2((double) st.hi - (double) nhi);
+        const float nhi = ref_exponent(wm);
+        if (st.m > -INFINITY) st.s = rescale(st.s, st.hi, nhi);
         st.m = wm;
         st.hi = nhi;
     }
@@ -465,69 +559,84 @@ __device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE]
 
 // The K-th largest key among the first `lim` entries of the buffer, by one wave (entries other waves have reserved
 // but not written yet read as 0 and are not counted); 0 when there are fewer than K. A bitwise search from the top
-// key bit down, each step counting the keys at or above the candidate with one ballot count per register.
+// key bit down, each candidate counted with one ballot per 64 keys: the first 1024 keys held in registers, those of a
+// longer buffer read again from LDS.
 __device__ __forceinline__ uint32_t buffer_bound(const uint64_t * cand, int lim, int K) {
-    constexpr int kMaxPerLane = 32;  // lim <= a buffer of 2048 entries
-    const int l = lane_id();
-    uint32_t keys[kMaxPerLane];
+    constexpr int kHeld = 16;
+    // the lane's keys: words 2(l + 64j) + 1, one address and immediate offsets; lane l holds key j when l < lim - 64j
+    int l = lane_id();
+    asm volatile("" : "+v"(l));  // formed here, where the bound is taken, not kept live across the stream
+    const uint32_t * kw = (const uint32_t *) cand + 2 * l + 1;
+    const int nj = (lim + kWave - 1) / kWave;
+    uint32_t keys[kHeld];
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; j++) {
-        const int i = l + kWave * j;
-        keys[j] = i < lim ? (uint32_t) (cand[i] >> 32) : 0u;
-    }
+    for (int j = 0; j < kHeld; j++) keys[j] = (j < nj && l < lim - kWave * j) ? kw[2 * kWave * j] : 0u;
     uint32_t key = 0;
     for (int b = 31; b >= 0; b--) {
         const uint32_t c = key | (1u << b);
         int cnt = 0;
 #pragma unroll
-        for (int j = 0; j < kMaxPerLane; j++) cnt += keys[j] >= c ? 1 : 0;
-        if (wave_sum_i32(cnt) >= K) key = c;
+        for (int j = 0; j < kHeld; j++)
+            if (j < nj) cnt += (int) __popcll(ballot(keys[j] >= c));
+        for (int j = kHeld; j < nj; j++) cnt += (int) __popcll(ballot(l < lim - kWave * j && kw[2 * kWave * j] >= c));
+        if (cnt >= K) key = c;
     }
     return key;
 }
 
 // Appends the passing elements of a step to the buffer: a ballot per element, one atomic per wave for the room,
-// each passing lane writing at its rank within its element's ballot. `all` (no bound yet) takes every valid element,
-// -inf ones included. The wave whose appends pass a multiple of 128 entries raises the work-group's threshold to the
-// K-th key of the buffer so far; every wave takes it up at its next step.
-template <int B, int VV, bool MASK>
+// each passing lane writing at its rank within its element's ballot and counting the entry in its bin. `all` (no
+// bound yet) takes every valid element, -inf ones included. The wave whose appends pass a multiple of 32 entries
+// raises the work-group's threshold from the bins; with no bins, or when the top bin holds a quarter of K (the
+// quotients run above the first step's largest), an exact search of the buffer does so at every 128 entries. Every
+// wave takes the threshold up at its next step.
+template <typename T, int B, int VV, bool MASK>
 __device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
-                                               const float (&q)[kE], const float (&x)[kE], uint32_t kill, int id_base,
+                                               const float (&q)[kE], const T * rowp, uint32_t kill, int id_base,
                                                bool all) {
-    uint64_t pm[kE];
+    // the ballots are taken twice (counted, then written) rather than held: they would take 32 scalar registers
+    auto pass = [&](int k) {
+        const bool live = !MASK || !((kill >> k) & 1u);
+        return ballot(all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau));
+    };
     int total = 0;
 #pragma unroll
-    for (int k = 0; k < kE; k++) {
-        const bool live = !MASK || !((kill >> k) & 1u);
-        pm[k] = ballot(all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau));
-        total += (int) __popcll(pm[k]);
-    }
+    for (int k = 0; k < kE; k++) total += (int) __popcll(pass(k));
     if (total == 0) return;
     uint32_t base = 0;
     if (lane_id() == 0) base = atomicAdd(&ctl->n, (uint32_t) total);
     base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
     if (base + (uint32_t) total > (uint32_t) cap && lane_id() == 0) ctl->overflow = 1u;
+    const float blo = ctl->bin_lo, bscale = ctl->bin_scale;
+    const bool binned = bscale > 0.0f;
     int off = (int) base;
 #pragma unroll
     for (int k = 0; k < kE; k++) {
-        if (pm[k]) {
-            if ((pm[k] >> lane_id()) & 1ull) {
-                const int pos = off + lanes_below(pm[k]);
+        const uint64_t pm = pass(k);
+        if (pm) {
+            if ((pm >> lane_id()) & 1ull) {
+                const int pos = off + lanes_below(pm);
                 if (pos < cap) {
                     // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
-                    float qq = q[k];
-                    if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = x[k] / pl.t;
                     const int id = id_base + (k / VV) * (B * VV) + (k % VV);
+                    float qq = q[k];
+                    if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = load_one<T>(rowp + id) / pl.t;
                     cand[pos] = make_entry(order_key(qq), (uint32_t) id);
+                    if (binned) atomicAdd(&ctl->bins[value_bin(blo, bscale, qq)], 1u);
                 }
             }
-            off += (int) __popcll(pm[k]);
+            off += (int) __popcll(pm);
         }
     }
     const uint32_t end = base + (uint32_t) total;
-    if ((base >> 7) == (end >> 7)) return;
-    const uint32_t kk = buffer_bound(cand, min((int) (end & ~127u), cap), pl.K);
-    const float tn = uniform_f(kk ? key_float(kk) : -INFINITY);
+    if ((base >> 5) == (end >> 5)) return;
+    uint32_t held;
+    float tn = binned ? bin_bound(ctl, pl.K, held) : -INFINITY;
+    if ((base >> 7) != (end >> 7) && (!binned || ctl->bins[kBins - 1] * 4u >= (uint32_t) pl.K)) {
+        const uint32_t kk = buffer_bound(cand, min((int) (end & ~127u), cap), pl.K);
+        if (kk) tn = fmaxf(tn, key_float(kk));
+    }
+    tn = uniform_f(tn);
     if (tn > st.tau) {
         st.tau = tn;
         if (lane_id() == 0) atomicMax(&ctl->tau_key, order_key(tn));
@@ -535,10 +644,11 @@ __device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, C
 }
 
 // One group of kE final logits per lane. x: raw logits; kill: elements that are special tokens or out of range;
-// rdead: those out of range. Element k's token is id_base + (k / VV) * B * VV + k % VV.
-template <int B, int VV, bool MASK, bool BOOT>
+// rdead: those out of range. Element k's token is id_base + (k / VV) * B * VV + k % VV; rowp: the row's logits.
+template <typename T, int B, int VV, bool MASK, bool BOOT>
 __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
-                                            const float (&x)[kE], uint32_t kill, uint32_t rdead, int id_base) {
+                                            const float (&x)[kE], uint32_t kill, uint32_t rdead, int id_base,
+                                            const T * rowp) {
     float q[kE];
 #pragma unroll
     for (int k = 0; k < kE; k++) {
@@ -561,7 +671,7 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
 #pragma unroll
         for (int k = 0; k < w; k++) t[k] += t[k + w];
     }
-    if (ballot(!(t[0] <= 0x1p100f))) slow_group(pl, st, q, x, kill, MASK);
+    if (ballot(!(t[0] <= 0x1p100f))) slow_group<T, B, VV>(pl, st, q, rowp, id_base, kill, MASK);
     else st.s += (double) t[0];
     if (!BOOT && tk) st.tau = fmaxf(st.tau, uniform_f(key_float(tk)));
     // Candidates: one ballot per element against tau (NaN never passes); the appends only where a lane passes.
@@ -569,10 +679,10 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
         uint64_t any = 0;
 #pragma unroll
         for (int k = 0; k < kE; k++) any |= ballot(q[k] >= st.tau);
-        if (any) insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base, false);
+        if (any) insert_entries<T, B, VV, MASK>(pl, st, ctl, cand, cap, q, rowp, kill, id_base, false);
     } else {
         // no bound yet: every valid token of the chunk enters
-        insert_entries<B, VV, MASK>(pl, st, ctl, cand, cap, q, x, kill, id_base, true);
+        insert_entries<T, B, VV, MASK>(pl, st, ctl, cand, cap, q, rowp, kill, id_base, true);
     }
 }
 
@@ -657,25 +767,27 @@ struct StreamCtx {
     Ctl * ctl;
     uint64_t * cand;
     int cap;
+    const void * rowp;  // the row's logits
 };
 
-template <int B, int VV, bool MASK, bool BOOT, bool GREEDY>
+template <typename T, int B, int VV, bool MASK, bool BOOT, bool GREEDY>
 __device__ __forceinline__ void run_core(StreamCtx & c, const float (&x)[kE], uint32_t kill, uint32_t rdead, int id_base) {
     if constexpr (GREEDY) greedy_core<B, VV, MASK>(*c.pl, *c.g, x, kill, rdead, id_base);
-    else sample_core<B, VV, MASK, BOOT>(*c.pl, *c.st, c.ctl, c.cand, c.cap, x, kill, rdead, id_base);
+    else sample_core<T, B, VV, MASK, BOOT>(*c.pl, *c.st, c.ctl, c.cand, c.cap, x, kill, rdead, id_base, (const T *) c.rowp);
 }
 
-// The first step's vectors of a chunk (lanes past the last whole vector load it again; none when there is none).
+// A step's vectors of a chunk (lanes past the last whole vector load it again; none when the step has none).
 template <typename T, int B>
-__device__ inline void load_first(const Launch & a, const T * rowp, int c0, int c1, U32x4 (&first)[Elt<T>::U]) {
+__device__ __forceinline__ void load_step(const Launch & a, const T * rowp, int c0, int c1, int step,
+                                          U32x4 (&v)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V, U = Elt<T>::U;
     const int ng = a.vec_ok ? (c1 - c0) / V : 0;
     const U32x4 * vp = (const U32x4 *) (rowp + c0);
 #pragma unroll
-    for (int u = 0; u < U; u++) first[u] = U32x4{0u, 0u, 0u, 0u};
-    if (ng > 0) {
+    for (int u = 0; u < U; u++) v[u] = U32x4{0u, 0u, 0u, 0u};
+    if (ng > step * U * B) {
 #pragma unroll
-        for (int u = 0; u < U; u++) first[u] = vp[min((int) threadIdx.x + u * B, ng - 1)];
+        for (int u = 0; u < U; u++) v[u] = vp[min(step * U * B + (int) threadIdx.x + u * B, ng - 1)];
     }
 }
 
@@ -707,7 +819,7 @@ __device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int 
             rdead |= 1u << k;
         }
     }
-    run_core<B, 1, true, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + o0);
+    run_core<T, B, 1, true, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + o0);
 }
 
 // One step of the vector stream: U vectors per lane, vector g0 + u*B for u < U, of which those past the last whole
@@ -739,7 +851,7 @@ __device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T
 #pragma unroll
         for (int u = 0; u < U; u++) rdead |= (g0 + u * B < ng) ? 0u : (VM << (u * V));
     }
-    run_core<B, V, SPEC || RANGE, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + g0 * V);
+    run_core<T, B, V, SPEC || RANGE, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + g0 * V);
 }
 
 template <typename T, int B, bool SPEC, bool GREEDY>
@@ -763,14 +875,8 @@ __device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * r
     // the steady loop, whose loads for the next step are in flight while a step is worked on.
     U32x4 cur[U], nxt[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) {
-        cur[u] = first[u];  // loaded before the special tokens were built
-        nxt[u] = cur[u];
-    }
-    if (nit > 1) {
-#pragma unroll
-        for (int u = 0; u < U; u++) nxt[u] = vp[min(per + tid + u * B, gl)];
-    }
+    for (int u = 0; u < U; u++) cur[u] = first[u];  // requested before the special tokens were built
+    load_step<T, B>(a, rowp, c0, c1, 1, nxt);
     vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl, cap_vec);
     for (int it = 1; it + 1 < nit; it++) {
 #pragma unroll
@@ -1136,7 +1242,9 @@ __device__ inline void fb_visit(FbRow & r, F && f) {
         if (spec) {
             __syncthreads();  // the previous chunk's special tokens are read no more
             uint32_t bad = 0;
-            build_specials<B, V>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.red->i, bad);
+            HistIds<B> hist;
+            load_hist<B>(a, r.row, r.pl, hist, bad);
+            build_specials<B, V>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.red->i, hist);
         }
         for (int i = c0 + threadIdx.x; i < c1; i += B) {
             if (spec) {
@@ -1435,18 +1543,21 @@ __device__ inline void gather_append(const uint64_t * src, int n, uint64_t floor
 }
 
 // Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
-// their ids differ), reading the list as LDS broadcasts, two entries per read.
+// their ids differ), reading the list as LDS broadcasts, eight entries at a time.
 template <int B>
 __device__ inline void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
     for (int i = threadIdx.x; i < n; i += B) {
         const uint64_t e = src[i];
         int r = 0;
         int j = 0;
-        for (; j + 1 < n; j += 2) {
-            r += src[j] > e ? 1 : 0;
-            r += src[j + 1] > e ? 1 : 0;
+        for (; j + 8 <= n; j += 8) {
+            uint64_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = src[j + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) r += v[u] > e ? 1 : 0;
         }
-        if (j < n) r += src[j] > e ? 1 : 0;
+        for (; j < n; j++) r += src[j] > e ? 1 : 0;
         dst[r] = e;
     }
     __syncthreads();
@@ -1484,7 +1595,7 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     st.tau = -INFINITY;
     st.flags = 0;
     GreedySt g;
-    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, cand, cap};
+    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, cand, cap, rowp};
     if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1, first);
     else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1, first);
 
@@ -1515,44 +1626,50 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
             const bool fin = live && q > -INFINITY && q < INFINITY;
             const float wm = uniform_f(wave_max_f32(fin ? q : -INFINITY));
             if (wm > st.m) {
-                const float nhi = wm * kL2e;
-                if (st.m > -INFINITY) st.s *= exp2((double) st.hi - (double) nhi);
+                const float nhi = ref_exponent(wm);
+                if (st.m > -INFINITY) st.s = rescale(st.s, st.hi, nhi);
                 st.m = wm;
                 st.hi = nhi;
             }
             if (fin) st.s += (double) __builtin_amdgcn_exp2f(__builtin_fmaf(q, kL2e, -st.hi));
             if (live && !__builtin_isnan(q) && q >= tau) {
                 const uint32_t pos = atomicAdd(&ctl->n, 1u);
-                if (pos < (uint32_t) cap) cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
-                else ctl->overflow = 1u;
+                if (pos < (uint32_t) cap) {
+                    cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
+                    if (ctl->bin_scale > 0.0f) atomicAdd(&ctl->bins[value_bin(ctl->bin_lo, ctl->bin_scale, q)], 1u);
+                } else {
+                    ctl->overflow = 1u;
+                }
             }
         }
     }
 
-    // The chunk's totals: each wave's sum relative to its m, corrected for the rounding of m*L, then the waves'.
+    // The chunk's totals: each wave's sum is relative to 2^hi, hi = ceil(m*L) an integer; moved to the largest
+    // exponent H by powers of two, then to the largest quotient M by one factor 2^(H - M*L).
     {
-        double ws = wave_sum_f64(st.s);
-        if (st.m > -INFINITY) ws *= exp2(-(double) __builtin_fmaf(st.m, kL2e, -st.hi));
-        else ws = 0.0;
+        const double ws = wave_sum_f64(st.s);
         const uint32_t wf = wave_or_u32(st.flags);
         const uint32_t f0 = (c0 == 0 && tid == 0) ? nan0_flag<T>(rowp, pl, sp, banned_row) : 0u;
         if (lane == 0) {
-            red->d[wave] = ws;
+            red->d[wave] = st.m > -INFINITY ? ws : 0.0;
             red->f[wave] = st.m;
+            red->f[32 + wave] = st.hi;
             red->w[wave] = wf | f0;
         }
         if (tid == 0) ctl->ncomp = 0;
     }
     __syncthreads();
-    float M = -INFINITY;
+    float M = -INFINITY, H = -FLT_MAX;
     uint32_t F = bad;
     for (int w = 0; w < W; w++) {
         M = fmaxf(M, red->f[w]);
+        if (red->f[w] > -INFINITY) H = fmaxf(H, red->f[32 + w]);
         F |= red->w[w];
     }
     double S = 0.0;
     for (int w = 0; w < W; w++)
-        if (red->f[w] > -INFINITY) S += red->d[w] * exp((double) red->f[w] - (double) M);
+        if (red->f[w] > -INFINITY) S += rescale(red->d[w], red->f[32 + w], H);
+    if (M > -INFINITY) S *= exp2(-(double) __builtin_fmaf(M, kL2e, -H));
     // A finite quotient has a term above 0 against the largest one: S > 0. Every logit that is not finite, and every
     // finite one whose quotient is not (the correction step gives NaN for both), went through the exact path, which
     // set the flags.
@@ -1564,10 +1681,17 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     const int nb = min((int) nres, cap);
     const uint32_t tkey = ctl->tau_key;
     const bool complete = tkey <= order_key(-INFINITY) && !overflow;  // the threshold never left -inf
-    // The chunk's K-th key, by wave 0: every token at or above it is in the buffer (it is at or above every
-    // threshold the stream had), and at least K entries are.
+    // The chunk's floor, by wave 0: at or above every threshold the stream had (every token at or above it is in
+    // the buffer), with at least K entries at or above it: from the bins, or the exact K-th key where the bins would
+    // leave more than the sort takes.
     if (!complete && tid < kWave) {
-        const uint32_t kk = buffer_bound(cand, nb, pl.K);
+        uint32_t kk = 0;
+        if (ctl->bin_scale > 0.0f) {
+            uint32_t held;
+            const float tb = bin_bound(ctl, pl.K, held);
+            if (tb > -INFINITY && held + 64u <= (uint32_t) kSortCap) kk = order_key(tb);
+        }
+        if (kk == 0) kk = buffer_bound(cand, nb, pl.K);
         if (tid == 0) ctl->kkey = kk;
     }
     __syncthreads();
@@ -1660,7 +1784,7 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
     g.xmin = INFINITY;
     g.nanb = 0;
     SampleSt st;
-    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, nullptr, 0};
+    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, nullptr, 0, rowp};
     if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1, first);
     else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1, first);
 
@@ -1738,6 +1862,12 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     int row, split;
     xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
     if (row >= a.rows) return;
+    const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
+    const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
+    // The first step's logits go out before anything else (they need only the row), then the row's parameters and
+    // history ids; the special tokens are built once both are in.
+    U32x4 first[Elt<T>::U];
+    load_step<T, B>(a, rowp, c0, c1, 0, first);
 
     spx_row_params p;
     if (a.params) {
@@ -1758,9 +1888,7 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
         if (split == 0 && tid == 0) write_row(a, row, -1, SPX_ROW_INVALID_PARAMS, 0);
         return;
     }
-    const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
     const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
-    const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
     Ctl * ctl = (Ctl *) (lds + a.off_ctl);
     Red * red = (Red *) (lds + a.off_red);
     const bool sampling = pl.mode != kGreedy;
@@ -1770,14 +1898,18 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
         ctl->tau_key = 0;
         ctl->overflow = 0;
         ctl->last = 0;
+        ctl->bin_lo = -INFINITY;
+        ctl->bin_scale = 0.0f;
+        ctl->bin_width = 0.0f;
     }
     if (sampling) {
         uint64_t * cand = (uint64_t *) (lds + a.off_cand);
         for (int i = tid; i < a.cand_cap; i += B) cand[i] = 0;
+        for (int i = tid; i < kBins; i += B) ctl->bins[i] = 0;
     }
-    // The first step's logits are on their way while the special tokens are built.
-    U32x4 first[Elt<T>::U];
-    load_first<T, B>(a, rowp, c0, c1, first);
+    uint32_t bad = 0;
+    HistIds<B> hist;
+    load_hist<B>(a, row, pl, hist, bad);
     Specials sp;
     sp.spec = (uint2 *) (lds + a.off_spec);
     sp.meta = (uint32_t *) (lds + a.off_meta);
@@ -1786,8 +1918,7 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     sp.cap = lds + a.off_cap;
     sp.n_slots = 0;
     sp.any = pl.pen || banned_row != nullptr;
-    uint32_t bad = 0;
-    if (sp.any) build_specials<B, V>(sp, a, row, c0, c1, pl, banned_row, red->i, bad);
+    if (sp.any) build_specials<B, V>(sp, a, row, c0, c1, pl, banned_row, red->i, hist);
     __syncthreads();
     if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
     else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
