@@ -4,19 +4,20 @@
 // batch alone would not fill the CUs) and reads the chunk's logits once, 16 bytes per lane per load with the next
 // step's loads in flight. Per step every lane holds 16 logits in registers and keeps, for the whole chunk:
 //   - the exact quotient q = l/t of each logit (Markstein's correction step, correctly rounded like the reference's
-//     float division), and the sum of exp(q - m) as one fma, one exp2 and one add per logit against a wave-uniform
-//     reference m, corrected exactly for the rounding of m*log2(e) at the end;
+//     float division), and the sum of exp(q - m) as one fma, one exp2 and one add per logit against 2^hi, hi an
+//     integer exponent at or above m*log2(e), so that sums move between references by powers of two;
 //   - every token whose quotient reaches the chunk's threshold tau, appended to one candidate buffer in LDS. tau
 //     starts at a bound taken from the first step's lane maxima (at least K tokens lie above it) and rises from a
-//     128-bucket histogram of the appended quotients, so appends become rare after the first steps;
+//     256-bin count of the appended quotients (an exact search of the buffer where the bins cannot bound it), so
+//     appends become rare after the first steps;
 //   - the special tokens (a penalized row's history and the banned ids) as a bitmap in LDS: they are masked to -inf
 //     with two bit operations per logit, and a history token's raw logit is captured for the penalty stage, which
 //     runs on the few hundred history tokens after the stream.
 // A logit whose term is not finite (NaN, infinities, a quotient out of range) sends its group of 16 to an exact path
 // that sets the flags the reference's checks read. After the stream the chunk's candidates at or above the final
-// tau are sorted and the row is finished by the flavor's rule (softmax weights in double, top-k/top-p, pick() with
-// the row's uniform) - by the chunk itself, or by the last chunk of the row to arrive, which merges the others'. A
-// row whose draw runs past the candidates held, or whose flags need every token, is resolved by the multi-pass path
+// threshold are sorted and the row is finished by the flavor's rule (softmax weights in double, top-k/top-p, pick()
+// with the row's uniform) - by the chunk itself, or by the last chunk of the row to arrive, which merges the others'.
+// A row whose draw runs past the candidates held, or whose flags need every token, is resolved by the multi-pass path
 // (exact radix selects over the whole row) in that same work-group.
 //
 // Citations are relative to the reference checkout (nyosegawa/speech.cpp 0.11.1).
