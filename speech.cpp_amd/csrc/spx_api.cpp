@@ -36,8 +36,9 @@ spx_status hip_fail(hipError_t e, const char * what) {
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
 // The launch shape and the kernel's LDS layout for one call: the control block, reduction scratch, the chunk's
-// special-token words, the history slots (index, rank, count, captured vector), the candidate buffer and the sorted
-// candidates (also the multi-pass path's radix histograms).
+// special-token words, its list of distinct history tokens, the frequency-count table (two words per entry, at
+// least twice as many entries as history ids), the candidate buffer and the sorted candidates (also the multi-pass
+// path's radix histograms).
 size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool has_hist, bool has_ban, int max_hist) {
     using namespace spx;
     size_t off = 0;
@@ -47,16 +48,14 @@ size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool ha
     off += 1280;
     const size_t words = (size_t) (chunk + 31) / 32;
     a.off_spec = (int) off;
-    if (has_hist || has_ban) off += align_up(words * 8, 16);
-    const size_t slots = has_hist ? (size_t) max_hist : 0;
-    a.off_meta = (int) off;
-    off += align_up(slots * 4, 16);
-    a.off_ufirst = (int) off;
-    off += align_up(slots * 4, 16);
-    a.off_cnt = (int) off;
-    off += align_up(slots * 4, 16);
-    a.off_cap = (int) off;
-    off += slots * 16;
+    if (has_hist || has_ban) off += align_up(words * 4, 16);
+    a.off_own = (int) off;
+    if (has_hist) off += align_up((size_t) max_hist * 4, 16);
+    size_t tab = 64;
+    while (tab < 2 * (size_t) max_hist) tab *= 2;
+    a.tab_mask = (int) tab - 1;
+    a.off_tab = (int) off;
+    if (has_hist) off += tab * 8;
     a.cand_cap = 2 * block;
     a.off_cand = (int) off;
     if (!greedy_only) off += (size_t) a.cand_cap * 8;

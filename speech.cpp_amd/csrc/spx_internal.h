@@ -60,8 +60,9 @@ struct Launch {
     int max_out;
     int block, splits, chunk, nwg;
     int cand_cap;  // entries of a chunk's candidate buffer
+    int tab_mask;  // entries of the frequency-count table - 1 (a power of two - 1)
     // LDS layout (byte offsets)
-    int off_ctl, off_red, off_spec, off_meta, off_ufirst, off_cnt, off_cap, off_cand, off_sort, lds_bytes;
+    int off_ctl, off_red, off_spec, off_own, off_tab, off_cand, off_sort, lds_bytes;
     // workspace
     uint32_t * counters;   // [max_rows], each back to 0 after its row's last chunk
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]

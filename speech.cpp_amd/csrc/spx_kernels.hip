@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 #include "../../include/spx_sampler.h"
 #include "spx_device.h"
 #include "spx_internal.h"
@@ -136,6 +138,21 @@ __device__ __forceinline__ float kill_to(float v, uint32_t kill, int k) {
     return __uint_as_float((mk & kNegInfBits) | (~mk & __float_as_uint(v)));
 }
 
+// kill_to for every element of a group, as two bit operations each (a sign-extending bit field extract and a
+// bit-field insert), written out so that they stay bit operations and take no scalar registers.
+template <int K>
+__device__ __forceinline__ float kill_bit(float v, uint32_t kill, uint32_t ninf) {
+    uint32_t mk, r;
+    asm("v_bfe_i32 %0, %1, %2, 1" : "=v"(mk) : "v"(kill), "n"(K));
+    asm("v_bfi_b32 %0, %1, %2, %3" : "=v"(r) : "v"(mk), "v"(ninf), "v"(__float_as_uint(v)));
+    return __uint_as_float(r);
+}
+template <int... K>
+__device__ __forceinline__ void kill_group(float * q, uint32_t kill, std::integer_sequence<int, K...>) {
+    const uint32_t ninf = kNegInfBits;
+    ((q[K] = kill_bit<K>(q[K], kill, ninf)), ...);
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // Work-group helpers
 // ------------------------------------------------------------------------------------------------------------------
@@ -214,6 +231,7 @@ struct Ctl {
     uint32_t resolved;  // the finishing wave settled the row
     uint32_t ncomp;     // candidates at or above the final threshold
     uint32_t kkey;      // the chunk's K-th key
+    uint32_t n_own;     // distinct history tokens listed
     // The bins of the candidates' quotients, set by the first step: bin (q - lo) * scale clamped to [0, kBins), a
     // bin `width` about 1 / scale wide; scale 0: no bins (the first step gave no finite bound), the threshold moves
     // by exact searches. Kept here rather than in registers: they are read where a candidate is appended.
@@ -227,19 +245,26 @@ static_assert(sizeof(Ctl) <= kCtlBytes, "the control block outgrows its LDS");
 // Special tokens of a chunk, in LDS
 // ------------------------------------------------------------------------------------------------------------------
 
-// For each 32 tokens a word pair: .x the special bits (history of a penalized row, or banned), .y the history
-// vectors among the word's 16-byte vectors (low 8 bits) and the slot of the first of them (bits 8..31). A slot holds
-// one history vector: its index and history bits, the rank of its first history token among the chunk's (for the
-// counts), and the vector's raw 16 bytes, which the stream captures.
+// Per 32 tokens of the chunk one word of special bits: a banned token, or a history token of a penalized row; the
+// stream masks them to -inf. The penalty stage takes the chunk's distinct history tokens (in range, not banned) from
+// a list, each once: the thread whose atomicOr set a token's bit first appends it. Rows with a frequency penalty also
+// count each token's occurrences, in an open-addressing table keyed by token.
 struct Specials {
-    uint2 * spec;
-    uint32_t * meta;    // per slot: (vector index << 8) | the vector's history bits
-    uint32_t * ufirst;  // per slot: rank of its first history token
-    uint32_t * cnt;     // per history token, by rank: its occurrences in the history
-    unsigned char * cap;
-    int n_slots;
+    uint32_t * kill;
+    int32_t * own;     // the distinct history tokens of the chunk
+    uint32_t * tab;    // frequency counts: tab[2i] the key (token + 1; 0 empty), tab[2i + 1] the count
+    int tab_mask;      // table entries - 1, a power of two - 1
+    int n_own;
     bool any;
 };
+
+__device__ inline void specials_at(Specials & sp, const Launch & a, unsigned char * lds) {
+    sp.kill = (uint32_t *) (lds + a.off_spec);
+    sp.own = (int32_t *) (lds + a.off_own);
+    sp.tab = (uint32_t *) (lds + a.off_tab);
+    sp.tab_mask = a.tab_mask;
+    sp.n_own = 0;
+}
 
 template <typename T>
 struct Elt;
@@ -253,15 +278,6 @@ struct Elt<uint16_t> {
     static constexpr int V = 8;
     static constexpr int U = 2;
 };
-
-// Bit v set where the v-th V-token vector of a word has a bit of h set.
-template <int V>
-__device__ inline uint32_t vec_mask(uint32_t h) {
-    uint32_t m = 0;
-#pragma unroll
-    for (int v = 0; v < 32 / V; v++) m |= ((h >> (v * V)) & ((1u << V) - 1u)) ? (1u << v) : 0u;
-    return m;
-}
 
 // History ids each thread holds: thread t the row's ids t, t + B, ... (a history is at most kMaxHist ids).
 template <int B>
@@ -289,76 +305,67 @@ __device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan 
     }
 }
 
-template <int B, int V>
-__device__ inline void build_specials(Specials & sp, const Launch & a, int row, int c0, int c1, const Plan & pl,
-                                      const uint32_t * banned_row, int * red, const HistIds<B> & hist) {
+__device__ __forceinline__ uint32_t token_hash(int t) { return (uint32_t) t * 2654435761u; }
+
+// One occurrence of token t in the frequency table.
+__device__ inline void count_add(const Specials & sp, int t) {
+    const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
+    for (int probe = 0; probe <= sp.tab_mask; probe++) {
+        const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
+        const uint32_t prev = atomicCAS(&sp.tab[2 * i], 0u, key);
+        if (prev == 0u || prev == key) {
+            atomicAdd(&sp.tab[2 * i + 1], 1u);
+            return;
+        }
+    }
+}
+
+// The occurrences of token t counted by count_add.
+__device__ inline int count_of(const Specials & sp, int t) {
+    const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
+    for (int probe = 0; probe <= sp.tab_mask; probe++) {
+        const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
+        const uint32_t k = sp.tab[2 * i];
+        if (k == key) return (int) sp.tab[2 * i + 1];
+        if (k == 0u) return 0;
+    }
+    return 0;
+}
+
+// The chunk's special bits, its list of distinct history tokens and (frequency rows) their counts. c0 is a multiple
+// of 64, so the chunk's words are whole words of the ban mask.
+template <int B>
+__device__ inline void build_specials(Specials & sp, int c0, int c1, const Plan & pl, const uint32_t * banned_row,
+                                      const HistIds<B> & hist, uint32_t * n_own) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
-    for (int w = tid; w < nw; w += B) sp.spec[w] = make_uint2(0u, 0u);
-    __syncthreads();
-    if (pl.pen) {
-        // the history bits, in .y for now
-#pragma unroll
-        for (int r = 0; r < HistIds<B>::R; r++) {
-            const int t = hist.id[r];
-            if (t >= c0 && t < c1) atomicOr(&sp.spec[(t - c0) >> 5].y, 1u << ((t - c0) & 31));
-        }
-        __syncthreads();
-    }
-    // Each thread takes a run of words: slots and history ranks by two scans, then the final word pairs.
-    const int wpt = (nw + B - 1) / B;
-    const int w0 = min(nw, tid * wpt), w1 = min(nw, w0 + wpt);
-    int nv = 0, nu = 0;
-    for (int w = w0; w < w1; w++) {
-        const uint32_t h = sp.spec[w].y;
-        nv += __popc(vec_mask<V>(h));
-        nu += __popc(h);
-    }
-    // one scan of both counts, each below 2^16 (a chunk holds at most max_hist <= kMaxHist history tokens)
-    int tot2;
-    const int base2 = block_excl_scan_i32<B>((nv << 16) | nu, red, tot2);
-    int vb = base2 >> 16, ub = base2 & 0xffff;
-    const int tv = tot2 >> 16, tu = tot2 & 0xffff;
-    for (int w = w0; w < w1; w++) {
-        const uint32_t h = sp.spec[w].y;
-        const uint32_t occ = vec_mask<V>(h);
+    for (int w = tid; w < nw; w += B) {
         uint32_t bw = 0;
         if (banned_row) {
             bw = banned_row[(c0 >> 5) + w];
             const int base = c0 + (w << 5);
             if (base + 32 > c1) bw &= (1u << (c1 - base)) - 1u;  // 0 < c1 - base < 32 here
         }
-        sp.spec[w] = make_uint2(h | bw, ((uint32_t) vb << 8) | occ);
-        uint32_t o = occ;
-        while (o) {
-            const int v = __builtin_ctz(o);
-            o &= o - 1;
-            const uint32_t hm = (h >> (v * V)) & ((1u << V) - 1u);
-            sp.meta[vb] = ((uint32_t) (w * (32 / V) + v) << 8) | hm;
-            sp.ufirst[vb] = (uint32_t) ub;
-            ub += __popc(hm);
-            vb++;
-        }
+        sp.kill[w] = bw;
     }
-    sp.n_slots = tv;
-    __syncthreads();
     if (pl.counts) {
-        for (int s = tid; s < tu; s += B) sp.cnt[s] = 0;
-        __syncthreads();
+        for (int i = tid; i <= 2 * sp.tab_mask + 1; i += B) sp.tab[i] = 0u;
+    }
+    if (tid == 0) *n_own = 0u;
+    __syncthreads();
+    if (pl.pen) {
 #pragma unroll
         for (int r = 0; r < HistIds<B>::R; r++) {
             const int t = hist.id[r];
             if (t >= c0 && t < c1) {
-                const int o = t - c0;
-                const uint32_t info = sp.spec[o >> 5].y;
-                const int vpos = (o & 31) / V;
-                const int slot = (int) (info >> 8) + __popc(info & ((1u << vpos) - 1u) & 0xffu);
-                const int jj = o & (V - 1);
-                const uint32_t hm = sp.meta[slot] & 0xffu;
-                atomicAdd(&sp.cnt[sp.ufirst[slot] + __popc(hm & ((1u << jj) - 1u))], 1u);
+                const uint32_t bit = 1u << ((t - c0) & 31);
+                const uint32_t old = atomicOr(&sp.kill[(t - c0) >> 5], bit);
+                if (!(old & bit)) sp.own[atomicAdd(n_own, 1u)] = t;
+                if (pl.counts) count_add(sp, t);
             }
         }
         __syncthreads();
+        sp.n_own = (int) *n_own;
     }
 }
 
@@ -373,38 +380,12 @@ __device__ inline float load_one<uint16_t>(const uint16_t * p) {
     return bf16_to_float(*p);
 }
 
+// A distinct history token's final logit: its raw logit, read again from memory, penalized.
 template <typename T>
-__device__ inline float cap_value(const unsigned char * slot, int j);
-template <>
-__device__ inline float cap_value<float>(const unsigned char * slot, int j) {
-    return ((const float *) slot)[j];
-}
-template <>
-__device__ inline float cap_value<uint16_t>(const unsigned char * slot, int j) {
-    return bf16_to_float(((const uint16_t *) slot)[j]);
-}
-
-// A history token of the chunk by its (slot, position) index: its id and final logit (penalized; -inf when banned).
-struct HistTok {
-    int id;
-    float v;
-    bool banned;
-};
-
-template <typename T, int V>
-__device__ inline bool hist_token(const Specials & sp, int i, int c0, const spx_row_params & p, const Plan & pl,
-                                  const uint32_t * banned_row, const T * rowp, bool captured, HistTok & h) {
-    const int s = i / V, j = i & (V - 1);
-    const uint32_t meta = sp.meta[s];
-    if (!((meta >> j) & 1u)) return false;
-    h.id = c0 + (int) (meta >> 8) * V + j;
-    const float raw = captured ? cap_value<T>(sp.cap + (size_t) s * 16, j) : load_one<T>(rowp + h.id);
-    const int c = pl.counts ? (int) sp.cnt[sp.ufirst[s] + __popc(meta & ((1u << j) - 1u) & 0xffu)] : 1;
-    float v = penalize(raw, c, p);
-    h.banned = banned_row && ((banned_row[h.id >> 5] >> (h.id & 31)) & 1u);
-    if (h.banned) v = -INFINITY;
-    h.v = v;
-    return true;
+__device__ inline float hist_value(const Specials & sp, int t, const spx_row_params & p, const Plan & pl,
+                                   const T * rowp) {
+    const int c = pl.counts ? count_of(sp, t) : 1;
+    return penalize(load_one<T>(rowp + t), c, p);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -657,10 +638,7 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
         const float q0 = x[k] * pl.rt;
         q[k] = __builtin_fmaf(__builtin_fmaf(-q0, pl.t, x[k]), pl.rt, q0);
     }
-    if (MASK) {
-#pragma unroll
-        for (int k = 0; k < kE; k++) q[k] = kill_to(q[k], kill, k);
-    }
+    if (MASK) kill_group(q, kill, std::make_integer_sequence<int, kE>{});
     if (BOOT) bootstrap<B>(pl, st, ctl, q);
     // the work-group's threshold, raised by whichever wave last refreshed it
     const uint32_t tk = BOOT ? 0u : __hip_atomic_load(&ctl->tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -703,7 +681,8 @@ __device__ __forceinline__ void greedy_core(const Plan & pl, GreedySt & g, const
                                             uint32_t rdead, int id_base) {
     float xm[kE];
 #pragma unroll
-    for (int k = 0; k < kE; k++) xm[k] = MASK ? kill_to(x[k], kill, k) : x[k];
+    for (int k = 0; k < kE; k++) xm[k] = x[k];
+    if (MASK) kill_group(xm, kill, std::make_integer_sequence<int, kE>{});
     if (pl.nanchk) {
 #pragma unroll
         for (int k = 0; k < kE; k++) g.nanb |= ballot(xm[k] != xm[k]);
@@ -762,7 +741,6 @@ __device__ inline void unpack<uint16_t>(const U32x4 & r, float * x) {
 struct StreamCtx {
     const Plan * pl;
     const Specials * sp;
-    bool cap_on;     // capture history vectors
     SampleSt * st;
     GreedySt * g;
     Ctl * ctl;
@@ -795,7 +773,6 @@ __device__ __forceinline__ void load_step(const Launch & a, const T * rowp, int 
 // kE tokens per lane, one each at chunk offsets o0 + k*B: rows that are not 16-byte aligned, and a chunk's tail.
 template <typename T, int B, bool SPEC, bool GREEDY, bool BOOT>
 __device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int c0, int n, int o0) {
-    constexpr int V = Elt<T>::V;
     float x[kE];
     uint32_t kill = 0, rdead = 0;
 #pragma unroll
@@ -805,17 +782,7 @@ __device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int 
         if (o < n) {
             const T raw = rowp[c0 + o];
             x[k] = load_one<T>(&raw);
-            if (SPEC) {
-                const uint2 pr = c.sp->spec[o >> 5];
-                if ((pr.x >> (o & 31)) & 1u) {
-                    kill |= 1u << k;
-                    const int vpos = (o & 31) / V;
-                    if (c.cap_on && ((pr.y >> vpos) & 1u)) {
-                        const int slot = (int) (pr.y >> 8) + __popc(pr.y & ((1u << vpos) - 1u));
-                        ((T *) (c.sp->cap + (size_t) slot * 16))[o & (V - 1)] = raw;
-                    }
-                }
-            }
+            if (SPEC && ((c.sp->kill[o >> 5] >> (o & 31)) & 1u)) kill |= 1u << k;
         } else {
             rdead |= 1u << k;
         }
@@ -824,29 +791,25 @@ __device__ __forceinline__ void scalar_group(StreamCtx & c, const T * rowp, int 
 }
 
 // One step of the vector stream: U vectors per lane, vector g0 + u*B for u < U, of which those past the last whole
-// vector (ng) are out of range when RANGE. Captures the history vectors; BOOT is the first step.
+// vector (ng) are out of range when RANGE; BOOT is the first step. A vector's special bits are V bits of one word.
 template <typename T, int B, bool SPEC, bool GREEDY, bool RANGE, bool BOOT>
-__device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T>::U], int c0, int g0, int ng, int gl,
-                                         bool cap_vec) {
+__device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T>::U], int c0, int g0, int ng, int gl) {
     constexpr int V = Elt<T>::V, U = Elt<T>::U, VW = 32 / V;
     constexpr uint32_t VM = (1u << V) - 1u;
-    float x[kE];
-#pragma unroll
-    for (int u = 0; u < U; u++) unpack<T>(cur[u], x + u * V);
     uint32_t kill = 0;
     if (SPEC) {
+        uint32_t kw[U];
 #pragma unroll
         for (int u = 0; u < U; u++) {
             const int gg = RANGE ? min(g0 + u * B, gl) : g0 + u * B;
-            const uint2 pr = c.sp->spec[gg / VW];
-            const int vpos = gg & (VW - 1);
-            kill |= ((pr.x >> (vpos * V)) & VM) << (u * V);
-            if (cap_vec && ((pr.y >> vpos) & 1u)) {
-                const int slot = (int) (pr.y >> 8) + __popc(pr.y & ((1u << vpos) - 1u));
-                *(U32x4 *) (c.sp->cap + (size_t) slot * 16) = cur[u];
-            }
+            kw[u] = c.sp->kill[gg / VW] >> ((gg & (VW - 1)) * V);
         }
+#pragma unroll
+        for (int u = 0; u < U; u++) kill |= (kw[u] & VM) << (u * V);
     }
+    float x[kE];
+#pragma unroll
+    for (int u = 0; u < U; u++) unpack<T>(cur[u], x + u * V);
     uint32_t rdead = 0;
     if (RANGE) {
 #pragma unroll
@@ -871,23 +834,22 @@ __device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * r
     const int nit = ng > 0 ? (ng + per - 1) / per : 1;
     const int gl = max(ng - 1, 0);
     const U32x4 * vp = (const U32x4 *) (rowp + c0);
-    const bool cap_vec = c.cap_on && ng > 0;
     // The first and last steps (lanes past the last vector load it again and take nothing from it) are peeled off
     // the steady loop, whose loads for the next step are in flight while a step is worked on.
     U32x4 cur[U], nxt[U];
 #pragma unroll
     for (int u = 0; u < U; u++) cur[u] = first[u];  // requested before the special tokens were built
     load_step<T, B>(a, rowp, c0, c1, 1, nxt);
-    vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl, cap_vec);
+    vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl);
     for (int it = 1; it + 1 < nit; it++) {
 #pragma unroll
         for (int u = 0; u < U; u++) cur[u] = nxt[u];
         const int g0 = it * per + tid;
 #pragma unroll
         for (int u = 0; u < U; u++) nxt[u] = vp[min(g0 + per + u * B, gl)];
-        vec_step<T, B, SPEC, GREEDY, false, false>(c, cur, c0, g0, ng, gl, cap_vec);
+        vec_step<T, B, SPEC, GREEDY, false, false>(c, cur, c0, g0, ng, gl);
     }
-    if (nit > 1) vec_step<T, B, SPEC, GREEDY, true, false>(c, nxt, c0, (nit - 1) * per + tid, ng, gl, cap_vec);
+    if (nit > 1) vec_step<T, B, SPEC, GREEDY, true, false>(c, nxt, c0, (nit - 1) * per + tid, ng, gl);
     if (n - ng * V > 0) scalar_group<T, B, SPEC, GREEDY, false>(c, rowp, c0, n, ng * V + tid);
 }
 
@@ -1227,13 +1189,13 @@ struct FbRow {
     const uint32_t * banned_row;
     float top;  // the largest final quotient
     Red * red;
+    uint32_t * n_own;
 };
 
 // Visits every token of the row, chunk by chunk, each chunk's special tokens rebuilt in LDS: f(entry, final logit,
 // quotient, banned, id), the entry 0 for a NaN quotient. A banned token is visited as -inf, once.
 template <typename T, int B, typename F>
 __device__ inline void fb_visit(FbRow & r, F && f) {
-    constexpr int V = Elt<T>::V;
     const Launch & a = *r.a;
     const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
     const bool spec = r.pl.pen || r.banned_row;
@@ -1245,12 +1207,12 @@ __device__ inline void fb_visit(FbRow & r, F && f) {
             uint32_t bad = 0;
             HistIds<B> hist;
             load_hist<B>(a, r.row, r.pl, hist, bad);
-            build_specials<B, V>(r.sp, a, r.row, c0, c1, r.pl, r.banned_row, r.red->i, hist);
+            build_specials<B>(r.sp, c0, c1, r.pl, r.banned_row, hist, r.n_own);
         }
         for (int i = c0 + threadIdx.x; i < c1; i += B) {
             if (spec) {
                 const int o = i - c0;
-                if ((r.sp.spec[o >> 5].x >> (o & 31)) & 1u) {
+                if ((r.sp.kill[o >> 5] >> (o & 31)) & 1u) {
                     // history tokens are visited below; a banned one (history or not) here
                     if (r.banned_row && ((r.banned_row[i >> 5] >> (i & 31)) & 1u))
                         f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
@@ -1262,11 +1224,11 @@ __device__ inline void fb_visit(FbRow & r, F && f) {
             f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
         }
         if (r.pl.pen) {
-            for (int k = threadIdx.x; k < r.sp.n_slots * V; k += B) {
-                HistTok h;
-                if (!hist_token<T, V>(r.sp, k, c0, r.p, r.pl, r.banned_row, rowp, false, h) || h.banned) continue;
-                const float q = div_rn(h.v, r.pl.t, r.pl.rt);
-                f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) h.id), h.v, q, false, h.id);
+            for (int k = threadIdx.x; k < r.sp.n_own; k += B) {
+                const int id = r.sp.own[k];
+                const float v = hist_value<T>(r.sp, id, r.p, r.pl, rowp);
+                const float q = div_rn(v, r.pl.t, r.pl.rt);
+                f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) id), v, q, false, id);
             }
         }
     }
@@ -1355,15 +1317,11 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
     r.p = p;
     r.pl = pl;
     r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
-    r.sp.spec = (uint2 *) (lds + a.off_spec);
-    r.sp.meta = (uint32_t *) (lds + a.off_meta);
-    r.sp.ufirst = (uint32_t *) (lds + a.off_ufirst);
-    r.sp.cnt = (uint32_t *) (lds + a.off_cnt);
-    r.sp.cap = lds + a.off_cap;
-    r.sp.n_slots = 0;
+    specials_at(r.sp, a, lds);
     r.sp.any = pl.pen || r.banned_row;
     r.top = 0.0f;
     r.red = red;
+    r.n_own = &((Ctl *) (lds + a.off_ctl))->n_own;
     // The flags, exactly, and the first and last entries of the order.
     uint32_t fl = 0;
     uint64_t hi_e = 0, lo_e = ~0ull;
@@ -1519,7 +1477,7 @@ __device__ inline bool arrive_last(const Launch & a, int row, Ctl * ctl) {
 template <typename T>
 __device__ inline uint32_t nan0_flag(const T * rowp, const Plan & pl, const Specials & sp, const uint32_t * banned_row) {
     const bool ban0 = banned_row && (banned_row[0] & 1u);
-    const bool hist0 = pl.pen && sp.any && (sp.spec[0].x & 1u) && !ban0;
+    const bool hist0 = pl.pen && sp.any && (sp.kill[0] & 1u) && !ban0;
     if (ban0 || hist0) return 0u;
     return __builtin_isnan(load_one<T>(rowp)) ? kNaN0 : 0u;
 }
@@ -1596,29 +1554,32 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     st.tau = -INFINITY;
     st.flags = 0;
     GreedySt g;
-    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, cand, cap, rowp};
+    StreamCtx c{&pl, &sp, &st, &g, ctl, cand, cap, rowp};
     if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1, first);
     else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1, first);
 
-    // The history tokens (penalties, the ban), one per thread, with the statistics and the threshold of the stream:
-    // a term against the wave's reference (raised first where a quotient passes it), the flags, an entry.
-    if (pl.pen && sp.n_slots > 0) {
-        __syncthreads();  // the captures and the stream's appends are done
-        const int npairs = sp.n_slots * V;
+    // The history tokens (the penalties), one per thread, with the statistics and the threshold of the stream: a
+    // term against the wave's reference (raised first where a quotient passes it), the flags, an entry.
+    if (pl.pen && sp.n_own > 0) {
+        __syncthreads();  // the stream's appends are done
         const uint32_t tk = ctl->tau_key;
         const float tau = tk ? key_float(tk) : -INFINITY;
-        for (int i0 = 0; i0 < npairs; i0 += B) {
+        for (int i0 = 0; i0 < sp.n_own; i0 += B) {
             const int i = i0 + tid;
-            HistTok h;
-            const bool ok = i < npairs && hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h);
-            const bool live = ok && !h.banned;
-            float q = -INFINITY;
-            if (ok && h.id == 0 && __builtin_isnan(h.v)) st.flags |= kNaN0;
+            const bool live = i < sp.n_own;
+            int hid = 0;
+            float hv = 0.0f;
             if (live) {
-                q = div_rn(h.v, pl.t, pl.rt);
-                if (__builtin_isnan(h.v)) st.flags |= kNaN;
-                else if (h.v == INFINITY) st.flags |= kPosInf;
-                else if (h.v == -INFINITY) st.flags |= kNegInf;
+                hid = sp.own[i];
+                hv = hist_value<T>(sp, hid, p, pl, rowp);
+            }
+            float q = -INFINITY;
+            if (live && hid == 0 && __builtin_isnan(hv)) st.flags |= kNaN0;
+            if (live) {
+                q = div_rn(hv, pl.t, pl.rt);
+                if (__builtin_isnan(hv)) st.flags |= kNaN;
+                else if (hv == INFINITY) st.flags |= kPosInf;
+                else if (hv == -INFINITY) st.flags |= kNegInf;
                 else {
                     st.flags |= kFinite;
                     if (!__builtin_isfinite(q)) st.flags |= kTempOver;
@@ -1636,7 +1597,7 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
             if (live && !__builtin_isnan(q) && q >= tau) {
                 const uint32_t pos = atomicAdd(&ctl->n, 1u);
                 if (pos < (uint32_t) cap) {
-                    cand[pos] = make_entry(order_key(q), (uint32_t) h.id);
+                    cand[pos] = make_entry(order_key(q), (uint32_t) hid);
                     if (ctl->bin_scale > 0.0f) atomicAdd(&ctl->bins[value_bin(ctl->bin_lo, ctl->bin_scale, q)], 1u);
                 } else {
                     ctl->overflow = 1u;
@@ -1785,7 +1746,7 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
     g.xmin = INFINITY;
     g.nanb = 0;
     SampleSt st;
-    StreamCtx c{&pl, &sp, pl.pen, &st, &g, ctl, nullptr, 0, rowp};
+    StreamCtx c{&pl, &sp, &st, &g, ctl, nullptr, 0, rowp};
     if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1, first);
     else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1, first);
 
@@ -1810,18 +1771,17 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
         F |= red->w[w];
     }
     __syncthreads();
-    if (pl.pen && sp.n_slots > 0) {
+    if (pl.pen && sp.n_own > 0) {
         uint64_t hb = 0;
         uint32_t hf = 0;
-        for (int i = tid; i < sp.n_slots * V; i += B) {
-            HistTok h;
-            if (!hist_token<T, V>(sp, i, c0, p, pl, banned_row, rowp, true, h)) continue;
-            if (h.id == 0 && __builtin_isnan(h.v)) hf |= kNaN0;
-            if (h.banned) continue;
-            if (__builtin_isnan(h.v)) hf |= kNaN;
-            else if (h.v == -INFINITY) hf |= kNegInf;
+        for (int i = tid; i < sp.n_own; i += B) {
+            const int hid = sp.own[i];
+            const float hv = hist_value<T>(sp, hid, p, pl, rowp);
+            if (hid == 0 && __builtin_isnan(hv)) hf |= kNaN0;
+            if (__builtin_isnan(hv)) hf |= kNaN;
+            else if (hv == -INFINITY) hf |= kNegInf;
             else {
-                const uint64_t e = make_entry(order_key(h.v), (uint32_t) h.id);
+                const uint64_t e = make_entry(order_key(hv), (uint32_t) hid);
                 hb = e > hb ? e : hb;
             }
         }
@@ -1912,14 +1872,9 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     HistIds<B> hist;
     load_hist<B>(a, row, pl, hist, bad);
     Specials sp;
-    sp.spec = (uint2 *) (lds + a.off_spec);
-    sp.meta = (uint32_t *) (lds + a.off_meta);
-    sp.ufirst = (uint32_t *) (lds + a.off_ufirst);
-    sp.cnt = (uint32_t *) (lds + a.off_cnt);
-    sp.cap = lds + a.off_cap;
-    sp.n_slots = 0;
+    specials_at(sp, a, lds);
     sp.any = pl.pen || banned_row != nullptr;
-    if (sp.any) build_specials<B, V>(sp, a, row, c0, c1, pl, banned_row, red->i, hist);
+    if (sp.any) build_specials<B>(sp, c0, c1, pl, banned_row, hist, &ctl->n_own);
     __syncthreads();
     if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
     else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
