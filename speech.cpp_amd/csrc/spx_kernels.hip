@@ -68,11 +68,11 @@ struct Plan {
     bool nanchk;  // greedy: look for NaN among the final logits
 };
 
-__device__ inline bool neutral(const spx_row_params & p) {
+__device__ __forceinline__ bool neutral(const spx_row_params & p) {
     return p.repetition_penalty == 1.0f && p.presence_penalty == 0.0f && p.frequency_penalty == 0.0f;
 }
 
-__device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_ban, bool has_hist) {
+__device__ __forceinline__ Plan make_plan(const spx_row_params & p, int vocab, bool has_ban, bool has_hist) {
     Plan pl;
     pl.flavor = p.flavor;
     pl.top_p = p.top_p;
@@ -119,7 +119,7 @@ __device__ inline Plan make_plan(const spx_row_params & p, int vocab, bool has_b
 
 // The penalty stage on one history token's raw logit: presence/frequency (no reference counterpart), then
 // restricted()'s repetition penalty once (src/families/qwen3-tts/sampler.cpp:37).
-__device__ inline float penalize(float x, int count, const spx_row_params & p) {
+__device__ __forceinline__ float penalize(float x, int count, const spx_row_params & p) {
     if (count > 0) {
         if (p.frequency_penalty != 0.0f) x = __fsub_rn(x, __fmul_rn(p.frequency_penalty, (float) count));
         if (p.presence_penalty != 0.0f) x = __fsub_rn(x, p.presence_penalty);
@@ -167,7 +167,7 @@ struct Red {
 };
 
 template <int B>
-__device__ inline int block_excl_scan_i32(int v, int * red, int & total) {
+__device__ __forceinline__ int block_excl_scan_i32(int v, int * red, int & total) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     const int inc = wave_incl_scan_i32(v);
     if (lane == kWave - 1) red[wave] = inc;
@@ -184,7 +184,7 @@ __device__ inline int block_excl_scan_i32(int v, int * red, int & total) {
 }
 
 template <int B>
-__device__ inline uint32_t block_or_u32(uint32_t v, uint32_t * red) {
+__device__ __forceinline__ uint32_t block_or_u32(uint32_t v, uint32_t * red) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     v = wave_or_u32(v);
     if (lane == 0) red[wave] = v;
@@ -196,7 +196,7 @@ __device__ inline uint32_t block_or_u32(uint32_t v, uint32_t * red) {
 }
 
 template <int B>
-__device__ inline uint64_t block_max_u64(uint64_t v, uint64_t * red) {
+__device__ __forceinline__ uint64_t block_max_u64(uint64_t v, uint64_t * red) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     v = wave_max_u64(v);
     if (lane == 0) red[wave] = v;
@@ -208,7 +208,7 @@ __device__ inline uint64_t block_max_u64(uint64_t v, uint64_t * red) {
 }
 
 template <int B>
-__device__ inline uint64_t block_min_u64(uint64_t v, uint64_t * red) {
+__device__ __forceinline__ uint64_t block_min_u64(uint64_t v, uint64_t * red) {
     const int lane = lane_id(), wave = threadIdx.x / kWave;
     v = wave_min_u64(v);
     if (lane == 0) red[wave] = v;
@@ -258,7 +258,7 @@ struct Specials {
     bool any;
 };
 
-__device__ inline void specials_at(Specials & sp, const Launch & a, unsigned char * lds) {
+__device__ __forceinline__ void specials_at(Specials & sp, const Launch & a, unsigned char * lds) {
     sp.kill = (uint32_t *) (lds + a.off_spec);
     sp.own = (int32_t *) (lds + a.off_own);
     sp.tab = (uint32_t *) (lds + a.off_tab);
@@ -308,7 +308,7 @@ __device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan 
 __device__ __forceinline__ uint32_t token_hash(int t) { return (uint32_t) t * 2654435761u; }
 
 // One occurrence of token t in the frequency table.
-__device__ inline void count_add(const Specials & sp, int t) {
+__device__ __forceinline__ void count_add(const Specials & sp, int t) {
     const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
     for (int probe = 0; probe <= sp.tab_mask; probe++) {
         const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
@@ -321,7 +321,7 @@ __device__ inline void count_add(const Specials & sp, int t) {
 }
 
 // The occurrences of token t counted by count_add.
-__device__ inline int count_of(const Specials & sp, int t) {
+__device__ __forceinline__ int count_of(const Specials & sp, int t) {
     const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
     for (int probe = 0; probe <= sp.tab_mask; probe++) {
         const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
@@ -335,7 +335,7 @@ __device__ inline int count_of(const Specials & sp, int t) {
 // The chunk's special bits, its list of distinct history tokens and (frequency rows) their counts. c0 is a multiple
 // of 64, so the chunk's words are whole words of the ban mask.
 template <int B>
-__device__ inline void build_specials(Specials & sp, int c0, int c1, const Plan & pl, const uint32_t * banned_row,
+__device__ __forceinline__ void build_specials(Specials & sp, int c0, int c1, const Plan & pl, const uint32_t * banned_row,
                                       const HistIds<B> & hist, uint32_t * n_own) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
@@ -370,19 +370,19 @@ __device__ inline void build_specials(Specials & sp, int c0, int c1, const Plan 
 }
 
 template <typename T>
-__device__ inline float load_one(const T * p);
+__device__ __forceinline__ float load_one(const T * p);
 template <>
-__device__ inline float load_one<float>(const float * p) {
+__device__ __forceinline__ float load_one<float>(const float * p) {
     return *p;
 }
 template <>
-__device__ inline float load_one<uint16_t>(const uint16_t * p) {
+__device__ __forceinline__ float load_one<uint16_t>(const uint16_t * p) {
     return bf16_to_float(*p);
 }
 
 // A distinct history token's final logit: its raw logit, read again from memory, penalized.
 template <typename T>
-__device__ inline float hist_value(const Specials & sp, int t, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ float hist_value(const Specials & sp, int t, const spx_row_params & p, const Plan & pl,
                                    const T * rowp) {
     const int c = pl.counts ? count_of(sp, t) : 1;
     return penalize(load_one<T>(rowp + t), c, p);
@@ -504,7 +504,7 @@ __device__ __forceinline__ void bootstrap(const Plan & pl, SampleSt & st, Ctl * 
 // finite quotient passes the old one, and the group's sum again. The logits are read again (element k is token
 // id_base + (k / VV) * B * VV + k % VV): the stream does not keep them past the quotients.
 template <typename T, int B, int VV>
-__device__ inline void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE], const T * rowp, int id_base,
+__device__ __forceinline__ void slow_group(const Plan & pl, SampleSt & st, float (&q)[kE], const T * rowp, int id_base,
                                   uint32_t kill, bool mask) {
     float gm = -INFINITY;
     uint32_t fl = 0;
@@ -639,6 +639,8 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
         q[k] = __builtin_fmaf(__builtin_fmaf(-q0, pl.t, x[k]), pl.rt, q0);
     }
     if (MASK) kill_group(q, kill, std::make_integer_sequence<int, kE>{});
+    // token 0's final logit, where it is not special, for std::max_element's NaN in front
+    if (BOOT && id_base == 0 && !(kill & 1u) && __builtin_isnan(x[0])) st.flags |= kNaN0;
     if (BOOT) bootstrap<B>(pl, st, ctl, q);
     // the work-group's threshold, raised by whichever wave last refreshed it
     const uint32_t tk = BOOT ? 0u : __hip_atomic_load(&ctl->tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
@@ -718,16 +720,16 @@ __device__ __forceinline__ void greedy_core(const Plan & pl, GreedySt & g, const
 using U32x4 = uint32_t __attribute__((ext_vector_type(4)));
 
 template <typename T>
-__device__ inline void unpack(const U32x4 & r, float * x);
+__device__ __forceinline__ void unpack(const U32x4 & r, float * x);
 template <>
-__device__ inline void unpack<float>(const U32x4 & r, float * x) {
+__device__ __forceinline__ void unpack<float>(const U32x4 & r, float * x) {
     x[0] = __uint_as_float(r.x);
     x[1] = __uint_as_float(r.y);
     x[2] = __uint_as_float(r.z);
     x[3] = __uint_as_float(r.w);
 }
 template <>
-__device__ inline void unpack<uint16_t>(const U32x4 & r, float * x) {
+__device__ __forceinline__ void unpack<uint16_t>(const U32x4 & r, float * x) {
     x[0] = __uint_as_float(r.x << 16);
     x[1] = __uint_as_float(r.x & 0xffff0000u);
     x[2] = __uint_as_float(r.y << 16);
@@ -818,14 +820,16 @@ __device__ __forceinline__ void vec_step(StreamCtx & c, const U32x4 (&cur)[Elt<T
     run_core<T, B, V, SPEC || RANGE, BOOT, GREEDY>(c, x, kill | rdead, rdead, c0 + g0 * V);
 }
 
-template <typename T, int B, bool SPEC, bool GREEDY>
-__device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * rowp, int c0, int c1,
-                                    const U32x4 (&first)[Elt<T>::U]) {
+// The chunk's stream; after_first() runs once the first step is done (its bound and bins are set).
+template <typename T, int B, bool SPEC, bool GREEDY, typename F>
+__device__ __forceinline__ void stream_chunk(StreamCtx & c, const Launch & a, const T * rowp, int c0, int c1,
+                                    const U32x4 (&first)[Elt<T>::U], F && after_first) {
     constexpr int V = Elt<T>::V, U = Elt<T>::U;
     const int n = c1 - c0, tid = threadIdx.x;
     if (!a.vec_ok) {
         const int nit = max(1, (n + kE * B - 1) / (kE * B));
         scalar_group<T, B, SPEC, GREEDY, true>(c, rowp, c0, n, tid);
+        after_first();
         for (int it = 1; it < nit; it++) scalar_group<T, B, SPEC, GREEDY, false>(c, rowp, c0, n, it * kE * B + tid);
         return;
     }
@@ -841,6 +845,7 @@ __device__ inline void stream_chunk(StreamCtx & c, const Launch & a, const T * r
     for (int u = 0; u < U; u++) cur[u] = first[u];  // requested before the special tokens were built
     load_step<T, B>(a, rowp, c0, c1, 1, nxt);
     vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl);
+    after_first();
     for (int it = 1; it + 1 < nit; it++) {
 #pragma unroll
         for (int u = 0; u < U; u++) cur[u] = nxt[u];
@@ -865,7 +870,7 @@ struct RowTotals {
 };
 
 // The row status, as the reference's checks order them; -1 when the row goes on.
-__device__ inline int row_status(const Plan & pl, const spx_row_params & p, uint32_t f, bool top_finite) {
+__device__ __forceinline__ int row_status(const Plan & pl, const spx_row_params & p, uint32_t f, bool top_finite) {
     if (pl.mode == kInvalid || (f & kBadHist)) return SPX_ROW_INVALID_PARAMS;
     const bool pen = !neutral(p);
     const bool posinf = (f & kPosInf) != 0;
@@ -893,14 +898,14 @@ __device__ inline int row_status(const Plan & pl, const spx_row_params & p, uint
     return -1;
 }
 
-__device__ inline void write_row(const Launch & a, int row, int id, int status, int kept) {
+__device__ __forceinline__ void write_row(const Launch & a, int row, int id, int status, int kept) {
     a.out_ids[row] = status == SPX_ROW_OK ? id : -1;
     if (a.out_status) a.out_status[row] = status;
     if (a.out_kept) a.out_kept[row] = status == SPX_ROW_OK ? kept : 0;
 }
 
 // The flags a greedy row's largest entry settles.
-__device__ inline uint32_t best_flags(uint64_t best) {
+__device__ __forceinline__ uint32_t best_flags(uint64_t best) {
     if (!best) return 0u;
     const float v = entry_value(best);
     return v == INFINITY ? kPosInf : (v > -INFINITY ? kFinite : 0u);
@@ -915,7 +920,7 @@ struct Cum4 {
     double c[4];
 };
 // Inclusive running sums over the elements in their order.
-__device__ inline Cum4 wave_cum4(const double (&x)[4]) {
+__device__ __forceinline__ Cum4 wave_cum4(const double (&x)[4]) {
     Cum4 r;
     r.c[0] = x[0];
     r.c[1] = r.c[0] + x[1];
@@ -927,7 +932,7 @@ __device__ inline Cum4 wave_cum4(const double (&x)[4]) {
     return r;
 }
 // The first element whose predicate holds (kNone when none).
-__device__ inline int wave_first4(const bool (&pred)[4]) {
+__device__ __forceinline__ int wave_first4(const bool (&pred)[4]) {
     int fj = 4;
     for (int j = 3; j >= 0; j--) fj = pred[j] ? j : fj;
     const uint64_t m = ballot(fj < 4);
@@ -935,12 +940,12 @@ __device__ inline int wave_first4(const bool (&pred)[4]) {
     const int l = (int) __builtin_ctzll(m);
     return 4 * l + __builtin_amdgcn_readlane(fj, l);
 }
-__device__ inline double wave_sum4(const double (&x)[4]) { return wave_sum_f64((x[0] + x[1]) + (x[2] + x[3])); }
+__device__ __forceinline__ double wave_sum4(const double (&x)[4]) { return wave_sum_f64((x[0] + x[1]) + (x[2] + x[3])); }
 
 // Finishes a row from its totals and its n sorted top entries e[0..n), n <= kFinishMax, in one wave (the caller's
 // wave 0). Returns true when the row is done, false when it needs the multi-pass path (its top-p set or its draw
 // runs beyond the entries held). pf: LDS scratch of kFinishMax floats.
-__device__ inline bool finish_wave(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
                                    const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf) {
     const int lane = lane_id();
     const double u = a.u ? a.u[row] : 0.0;
@@ -1146,7 +1151,7 @@ __device__ inline bool finish_wave(const Launch & a, int row, const spx_row_para
 
 // Wave 0 finishes the row; the work-group learns whether it must take the multi-pass path.
 template <int B>
-__device__ inline bool finish_block(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ bool finish_block(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
                                     const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf,
                                     Ctl * ctl) {
     if (threadIdx.x < kWave) {
@@ -1195,7 +1200,7 @@ struct FbRow {
 // Visits every token of the row, chunk by chunk, each chunk's special tokens rebuilt in LDS: f(entry, final logit,
 // quotient, banned, id), the entry 0 for a NaN quotient. A banned token is visited as -inf, once.
 template <typename T, int B, typename F>
-__device__ inline void fb_visit(FbRow & r, F && f) {
+__device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
     const Launch & a = *r.a;
     const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
     const bool spec = r.pl.pen || r.banned_row;
@@ -1238,7 +1243,7 @@ __device__ inline void fb_visit(FbRow & r, F && f) {
 // The first entry in falling order whose running count (by_mass false) or running mass reaches `target` (strict:
 // passes it), by radix passes of 8 bits over the 64-bit entries. False when no entry does.
 template <typename T, int B>
-__device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool strict, Select & out,
+__device__ __forceinline__ bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool strict, Select & out,
                                  uint32_t * hist_n, unsigned long long * hist_m) {
     int * ired = r.red->i;
     Select s;
@@ -1305,7 +1310,7 @@ __device__ inline bool fb_select(FbRow & r, bool by_mass, uint64_t target, bool 
 // whole row: the flags and the row status, then radix selects. `extra` carries the flags found before (a history
 // longer than the handle allows).
 template <typename T, int B>
-__device__ inline void fallback_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ void fallback_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
                                     uint32_t extra, unsigned char * lds) {
     const int tid = threadIdx.x;
     Red * red = (Red *) (lds + a.off_red);
@@ -1442,7 +1447,7 @@ __device__ inline void fallback_row(const Launch & a, int row, const spx_row_par
 // Chunks and rows
 // ------------------------------------------------------------------------------------------------------------------
 
-__device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & split) {
+__device__ __forceinline__ void xcd_map(int bid, int nwg, int splits, int & row, int & split) {
     // Work-groups are dispatched round-robin over the 8 XCDs; give the chunks of one row consecutive slots of one
     // XCD, so that the partials the last chunk reads were written through the same L2.
     const int x = bid & 7, l = bid >> 3;
@@ -1456,7 +1461,7 @@ __device__ inline void xcd_map(int bid, int nwg, int splits, int & row, int & sp
 // XCD written back), one atomic per chunk; true in the row's last chunk, whose acquire (its caches invalidated) lets
 // every thread then read the other chunks' partials. The other waves take no fence.
 template <int B>
-__device__ inline bool arrive_last(const Launch & a, int row, Ctl * ctl) {
+__device__ __forceinline__ bool arrive_last(const Launch & a, int row, Ctl * ctl) {
     if (threadIdx.x < kWave) {
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
         if (threadIdx.x == 0) {
@@ -1475,7 +1480,7 @@ __device__ inline bool arrive_last(const Launch & a, int row, Ctl * ctl) {
 
 // Token 0's final logit, where it is not a history token, for std::max_element's NaN in front.
 template <typename T>
-__device__ inline uint32_t nan0_flag(const T * rowp, const Plan & pl, const Specials & sp, const uint32_t * banned_row) {
+__device__ __forceinline__ uint32_t nan0_flag(const T * rowp, const Plan & pl, const Specials & sp, const uint32_t * banned_row) {
     const bool ban0 = banned_row && (banned_row[0] & 1u);
     const bool hist0 = pl.pen && sp.any && (sp.kill[0] & 1u) && !ban0;
     if (ban0 || hist0) return 0u;
@@ -1485,7 +1490,7 @@ __device__ inline uint32_t nan0_flag(const T * rowp, const Plan & pl, const Spec
 // Appends the entries of src[0..n) at or above `floor` to dst (at most kSortCap), one wave at a time per 64: a ballot,
 // one atomic per wave on the LDS count, no barrier. The order among the appended is free; the caller sorts.
 template <int B>
-__device__ inline void gather_append(const uint64_t * src, int n, uint64_t floor, uint64_t * dst, uint32_t * count) {
+__device__ __forceinline__ void gather_append(const uint64_t * src, int n, uint64_t floor, uint64_t * dst, uint32_t * count) {
     const int lane = lane_id();
     for (int i0 = (threadIdx.x / kWave) * kWave; i0 < n; i0 += B) {
         const int i = i0 + lane;
@@ -1504,7 +1509,7 @@ __device__ inline void gather_append(const uint64_t * src, int n, uint64_t floor
 // Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
 // their ids differ), reading the list as LDS broadcasts, eight entries at a time.
 template <int B>
-__device__ inline void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
+__device__ __forceinline__ void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
     for (int i = threadIdx.x; i < n; i += B) {
         const uint64_t e = src[i];
         int r = 0;
@@ -1525,7 +1530,7 @@ __device__ inline void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
 // The chunk's candidates at or above `floor`, gathered from buf[0..nb) and sorted into dst; returns how many there
 // are (beyond kSortCap only the count is exact).
 template <int B>
-__device__ inline int gather_sort(const uint64_t * buf, int nb, uint64_t floor, uint64_t * tmp, uint64_t * dst,
+__device__ __forceinline__ int gather_sort(const uint64_t * buf, int nb, uint64_t floor, uint64_t * tmp, uint64_t * dst,
                                   uint32_t * count) {
     gather_append<B>(buf, nb, floor, tmp, count);
     __syncthreads();
@@ -1535,7 +1540,7 @@ __device__ inline int gather_sort(const uint64_t * buf, int nb, uint64_t floor, 
 }
 
 template <typename T, int B>
-__device__ inline void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
                                   uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V;
@@ -1555,14 +1560,17 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
     st.flags = 0;
     GreedySt g;
     StreamCtx c{&pl, &sp, &st, &g, ctl, cand, cap, rowp};
-    if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1, first);
-    else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1, first);
 
-    // The history tokens (the penalties), one per thread, with the statistics and the threshold of the stream: a
-    // term against the wave's reference (raised first where a quotient passes it), the flags, an entry.
-    if (pl.pen && sp.n_own > 0) {
-        __syncthreads();  // the stream's appends are done
-        const uint32_t tk = ctl->tau_key;
+    // The history tokens (the penalties), one per thread, once the first step has set the bound and the bins: their
+    // raw logits read again (the first of each thread's requested before the stream), a term against the wave's
+    // reference (raised first where a quotient passes it), the flags, and an entry where the quotient reaches the
+    // threshold of the moment (it only rises, so every token at or above the final one is kept).
+    const bool hist_pass = pl.pen && sp.n_own > 0;
+    float raw0 = 0.0f;
+    if (hist_pass && tid < sp.n_own) raw0 = load_one<T>(rowp + sp.own[tid]);
+    auto history = [&]() __attribute__((always_inline)) {
+        if (!hist_pass) return;
+        const uint32_t tk = __hip_atomic_load(&ctl->tau_key, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
         const float tau = tk ? key_float(tk) : -INFINITY;
         for (int i0 = 0; i0 < sp.n_own; i0 += B) {
             const int i = i0 + tid;
@@ -1571,7 +1579,8 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
             float hv = 0.0f;
             if (live) {
                 hid = sp.own[i];
-                hv = hist_value<T>(sp, hid, p, pl, rowp);
+                const float raw = i0 == 0 ? raw0 : load_one<T>(rowp + hid);
+                hv = penalize(raw, pl.counts ? count_of(sp, hid) : 1, p);
             }
             float q = -INFINITY;
             if (live && hid == 0 && __builtin_isnan(hv)) st.flags |= kNaN0;
@@ -1604,33 +1613,32 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
                 }
             }
         }
-    }
+    };
+    if (sp.any) stream_chunk<T, B, true, false>(c, a, rowp, c0, c1, first, history);
+    else stream_chunk<T, B, false, false>(c, a, rowp, c0, c1, first, history);
 
     // The chunk's totals: each wave's sum is relative to 2^hi, hi = ceil(m*L) an integer; moved to the largest
     // exponent H by powers of two, then to the largest quotient M by one factor 2^(H - M*L).
     {
         const double ws = wave_sum_f64(st.s);
         const uint32_t wf = wave_or_u32(st.flags);
-        const uint32_t f0 = (c0 == 0 && tid == 0) ? nan0_flag<T>(rowp, pl, sp, banned_row) : 0u;
         if (lane == 0) {
             red->d[wave] = st.m > -INFINITY ? ws : 0.0;
             red->f[wave] = st.m;
             red->f[32 + wave] = st.hi;
-            red->w[wave] = wf | f0;
+            red->w[wave] = wf;
         }
         if (tid == 0) ctl->ncomp = 0;
     }
     __syncthreads();
-    float M = -INFINITY, H = -FLT_MAX;
-    uint32_t F = bad;
-    for (int w = 0; w < W; w++) {
-        M = fmaxf(M, red->f[w]);
-        if (red->f[w] > -INFINITY) H = fmaxf(H, red->f[32 + w]);
-        F |= red->w[w];
-    }
-    double S = 0.0;
-    for (int w = 0; w < W; w++)
-        if (red->f[w] > -INFINITY) S += rescale(red->d[w], red->f[32 + w], H);
+    // lane w < W takes wave w's values; every wave reduces them in the same order, so all agree on S, M and F
+    const bool has = lane < W;
+    const float mw = has ? red->f[lane] : -INFINITY;
+    const float hw = has && mw > -INFINITY ? red->f[32 + lane] : -FLT_MAX;
+    const float M = uniform_f(wave_max_f32(mw));
+    const float H = uniform_f(wave_max_f32(hw));
+    uint32_t F = bad | wave_or_u32(has ? red->w[lane] : 0u);
+    double S = wave_sum_f64(mw > -INFINITY ? rescale(red->d[lane], hw, H) : 0.0);
     if (M > -INFINITY) S *= exp2(-(double) __builtin_fmaf(M, kL2e, -H));
     // A finite quotient has a term above 0 against the largest one: S > 0. Every logit that is not finite, and every
     // finite one whose quotient is not (the correction step gives NaN for both), went through the exact path, which
@@ -1731,7 +1739,7 @@ __device__ inline void sample_row(const Launch & a, int row, int split, const sp
 }
 
 template <typename T, int B>
-__device__ inline void greedy_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ void greedy_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
                                   uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
     constexpr int V = Elt<T>::V;
@@ -1747,8 +1755,9 @@ __device__ inline void greedy_row(const Launch & a, int row, int split, const sp
     g.nanb = 0;
     SampleSt st;
     StreamCtx c{&pl, &sp, &st, &g, ctl, nullptr, 0, rowp};
-    if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1, first);
-    else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1, first);
+    auto none = []() __attribute__((always_inline)) {};
+    if (sp.any) stream_chunk<T, B, true, true>(c, a, rowp, c0, c1, first, none);
+    else stream_chunk<T, B, false, true>(c, a, rowp, c0, c1, first, none);
 
     {
         const uint64_t be = g.bi >= 0 ? make_entry(order_key(g.bx), (uint32_t) g.bi) : 0ull;
