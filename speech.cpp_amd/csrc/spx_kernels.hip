@@ -566,24 +566,26 @@ __device__ __forceinline__ uint32_t buffer_bound(const uint64_t * cand, int lim,
     return key;
 }
 
-// Appends the passing elements of a step to the buffer: a ballot per element, one atomic per wave for the room,
-// each passing lane writing at its rank within its element's ballot and counting the entry in its bin. `all` (no
-// bound yet) takes every valid element, -inf ones included. The wave whose appends pass a multiple of 32 entries
-// raises the work-group's threshold from the bins; with no bins, or when the top bin holds a quarter of K (the
-// quotients run above the first step's largest), an exact search of the buffer does so at every 128 entries. Every
-// wave takes the threshold up at its next step.
+// Appends the passing elements of a step to the buffer: each lane counts its own, a scan over the wave places them,
+// one atomic per wave takes the room, and each lane writes its elements in order and counts each in its bin. `all`
+// (no bound yet) takes every valid element, -inf ones included. The wave whose appends pass a multiple of 32 entries
+// raises the work-group's threshold from the bins; with no bins, or when the top bin alone holds K (the quotients
+// run so far above the first step's largest that the bins no longer tell them apart), an exact search of the buffer
+// does so at every 128 entries. Every wave takes the threshold up at its next step. Called by the whole wave.
 template <typename T, int B, int VV, bool MASK>
 __device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, Ctl * ctl, uint64_t * cand, int cap,
                                                const float (&q)[kE], const T * rowp, uint32_t kill, int id_base,
                                                bool all) {
-    // the ballots are taken twice (counted, then written) rather than held: they would take 32 scalar registers
+    float tau = uniform_f(st.tau);
     auto pass = [&](int k) {
         const bool live = !MASK || !((kill >> k) & 1u);
-        return ballot(all ? (live && !__builtin_isnan(q[k])) : (q[k] >= st.tau));
+        return all ? (live && !__builtin_isnan(q[k])) : (q[k] >= tau);
     };
-    int total = 0;
+    int cnt = 0;
 #pragma unroll
-    for (int k = 0; k < kE; k++) total += (int) __popcll(pass(k));
+    for (int k = 0; k < kE; k++) cnt += pass(k) ? 1 : 0;
+    const int incl = wave_incl_scan_i32(cnt);
+    const int total = __builtin_amdgcn_readlane(incl, kWave - 1);
     if (total == 0) return;
     uint32_t base = 0;
     if (lane_id() == 0) base = atomicAdd(&ctl->n, (uint32_t) total);
@@ -591,30 +593,28 @@ __device__ __forceinline__ void insert_entries(const Plan & pl, SampleSt & st, C
     if (base + (uint32_t) total > (uint32_t) cap && lane_id() == 0) ctl->overflow = 1u;
     const float blo = ctl->bin_lo, bscale = ctl->bin_scale;
     const bool binned = bscale > 0.0f;
-    int off = (int) base;
+    // the compares again, not their results of the count kept across it
+    asm volatile("" : "+s"(tau));
+    int pos = (int) base + incl - cnt;
 #pragma unroll
     for (int k = 0; k < kE; k++) {
-        const uint64_t pm = pass(k);
-        if (pm) {
-            if ((pm >> lane_id()) & 1ull) {
-                const int pos = off + lanes_below(pm);
-                if (pos < cap) {
-                    // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
-                    const int id = id_base + (k / VV) * (B * VV) + (k % VV);
-                    float qq = q[k];
-                    if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = load_one<T>(rowp + id) / pl.t;
-                    cand[pos] = make_entry(order_key(qq), (uint32_t) id);
-                    if (binned) atomicAdd(&ctl->bins[value_bin(blo, bscale, qq)], 1u);
-                }
+        if (pass(k)) {
+            if (pos < cap) {
+                // a quotient in the subnormal range: the division itself (the correction step assumes a normal one)
+                const int id = id_base + (k / VV) * (B * VV) + (k % VV);
+                float qq = q[k];
+                if (qq != 0.0f && __builtin_fabsf(qq) < 0x1p-125f) qq = load_one<T>(rowp + id) / pl.t;
+                cand[pos] = make_entry(order_key(qq), (uint32_t) id);
+                if (binned) atomicAdd(&ctl->bins[value_bin(blo, bscale, qq)], 1u);
             }
-            off += (int) __popcll(pm);
+            pos++;
         }
     }
     const uint32_t end = base + (uint32_t) total;
     if ((base >> 5) == (end >> 5)) return;
     uint32_t held;
     float tn = binned ? bin_bound(ctl, pl.K, held) : -INFINITY;
-    if ((base >> 7) != (end >> 7) && (!binned || ctl->bins[kBins - 1] * 4u >= (uint32_t) pl.K)) {
+    if ((base >> 7) != (end >> 7) && (!binned || ctl->bins[kBins - 1] >= (uint32_t) pl.K)) {
         const uint32_t kk = buffer_bound(cand, min((int) (end & ~127u), cap), pl.K);
         if (kk) tn = fmaxf(tn, key_float(kk));
     }
@@ -655,12 +655,13 @@ __device__ __forceinline__ void sample_core(const Plan & pl, SampleSt & st, Ctl 
     if (ballot(!(t[0] <= 0x1p100f))) slow_group<T, B, VV>(pl, st, q, rowp, id_base, kill, MASK);
     else st.s += (double) t[0];
     if (!BOOT && tk) st.tau = fmaxf(st.tau, uniform_f(key_float(tk)));
-    // Candidates: one ballot per element against tau (NaN never passes); the appends only where a lane passes.
+    // Candidates: the appends only where a lane's largest quotient reaches tau (a NaN is no lane's largest unless
+    // all of its are NaN, and never passes).
     if (st.tau > -INFINITY) {
-        uint64_t any = 0;
+        float lm = q[0];
 #pragma unroll
-        for (int k = 0; k < kE; k++) any |= ballot(q[k] >= st.tau);
-        if (any) insert_entries<T, B, VV, MASK>(pl, st, ctl, cand, cap, q, rowp, kill, id_base, false);
+        for (int k = 1; k < kE; k++) lm = fmaxf(lm, q[k]);
+        if (ballot(lm >= st.tau)) insert_entries<T, B, VV, MASK>(pl, st, ctl, cand, cap, q, rowp, kill, id_base, false);
     } else {
         // no bound yet: every valid token of the chunk enters
         insert_entries<T, B, VV, MASK>(pl, st, ctl, cand, cap, q, rowp, kill, id_base, true);
