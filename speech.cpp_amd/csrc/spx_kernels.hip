@@ -837,25 +837,40 @@ __device__ __forceinline__ void stream_chunk(StreamCtx & c, const Launch & a, co
     const int ng = n / V;  // whole vectors
     constexpr int per = U * B;
     const int nit = ng > 0 ? (ng + per - 1) / per : 1;
+    const int nfull = ng / per;  // steps without a lane past the last vector
     const int gl = max(ng - 1, 0);
     const U32x4 * vp = (const U32x4 *) (rowp + c0);
     // The first and last steps (lanes past the last vector load it again and take nothing from it) are peeled off
-    // the steady loop, whose loads for the next step are in flight while a step is worked on.
-    U32x4 cur[U], nxt[U];
+    // the steady loop, whose loads for the next step are in flight while a step is worked on. The steady loop takes
+    // two steps a turn, its two buffers trading places, while both steps it requests are whole (a lane's vectors at
+    // fixed offsets from the step's start); the rest go one step a turn.
+    U32x4 b0[U], b1[U];
 #pragma unroll
-    for (int u = 0; u < U; u++) cur[u] = first[u];  // requested before the special tokens were built
-    load_step<T, B>(a, rowp, c0, c1, 1, nxt);
-    vec_step<T, B, SPEC, GREEDY, true, true>(c, cur, c0, tid, ng, gl);
+    for (int u = 0; u < U; u++) b0[u] = first[u];  // requested before the special tokens were built
+    load_step<T, B>(a, rowp, c0, c1, 1, b1);
+    vec_step<T, B, SPEC, GREEDY, true, true>(c, b0, c0, tid, ng, gl);
     after_first();
-    for (int it = 1; it + 1 < nit; it++) {
+    int it = 1;
+    for (; it + 2 < nfull; it += 2) {
+        const U32x4 * s1 = vp + (it + 1) * per;
 #pragma unroll
-        for (int u = 0; u < U; u++) cur[u] = nxt[u];
+        for (int u = 0; u < U; u++) b0[u] = s1[tid + u * B];
+        vec_step<T, B, SPEC, GREEDY, false, false>(c, b1, c0, it * per + tid, ng, gl);
+        const U32x4 * s2 = vp + (it + 2) * per;
+#pragma unroll
+        for (int u = 0; u < U; u++) b1[u] = s2[tid + u * B];
+        vec_step<T, B, SPEC, GREEDY, false, false>(c, b0, c0, (it + 1) * per + tid, ng, gl);
+    }
+    for (; it + 1 < nit; it++) {
+        U32x4 cur[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) cur[u] = b1[u];
         const int g0 = it * per + tid;
 #pragma unroll
-        for (int u = 0; u < U; u++) nxt[u] = vp[min(g0 + per + u * B, gl)];
+        for (int u = 0; u < U; u++) b1[u] = vp[min(g0 + per + u * B, gl)];
         vec_step<T, B, SPEC, GREEDY, false, false>(c, cur, c0, g0, ng, gl);
     }
-    if (nit > 1) vec_step<T, B, SPEC, GREEDY, true, false>(c, nxt, c0, (nit - 1) * per + tid, ng, gl);
+    if (nit > 1) vec_step<T, B, SPEC, GREEDY, true, false>(c, b1, c0, (nit - 1) * per + tid, ng, gl);
     if (n - ng * V > 0) scalar_group<T, B, SPEC, GREEDY, false>(c, rowp, c0, n, ng * V + tid);
 }
 
