@@ -286,14 +286,13 @@ struct HistIds {
     int id[R];
 };
 
-// The row's history ids, requested ahead of the first step's logits (-1 past the row's history).
+// The row's history ids [h0, h1) of the history (-1 past the row's history).
 template <int B>
-__device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan & pl, HistIds<B> & h, uint32_t & bad) {
+__device__ __forceinline__ void load_hist_ids(const Launch & a, const Plan & pl, int h0, int h1, HistIds<B> & h,
+                                              uint32_t & bad) {
 #pragma unroll
     for (int r = 0; r < HistIds<B>::R; r++) h.id[r] = -1;
     if (!pl.pen) return;
-    const int h0 = a.hist_off[row];
-    int h1 = a.hist_off[row + 1];
     if (h1 - h0 > a.max_hist || h1 < h0) {
         bad |= kBadHist;
         h1 = h0;
@@ -303,6 +302,13 @@ __device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan 
         const int j = h0 + (int) threadIdx.x + r * B;
         if (j < h1) h.id[r] = a.hist[j];
     }
+}
+
+// The same, the row's offsets read here.
+template <int B>
+__device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan & pl, HistIds<B> & h, uint32_t & bad) {
+    const int h0 = pl.pen ? a.hist_off[row] : 0, h1 = pl.pen ? a.hist_off[row + 1] : 0;
+    load_hist_ids<B>(a, pl, h0, h1, h, bad);
 }
 
 __device__ __forceinline__ uint32_t token_hash(int t) { return (uint32_t) t * 2654435761u; }
@@ -1850,11 +1856,13 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     if (row >= a.rows) return;
     const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
     const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
-    // The first step's logits go out before anything else (they need only the row), then the row's parameters and
-    // history ids; the special tokens are built once both are in.
-    U32x4 first[Elt<T>::U];
-    load_step<T, B>(a, rowp, c0, c1, 0, first);
-
+    // The row's history offsets and parameters are requested first (they need only the row), then the first step's
+    // logits, then the history ids once their offsets are in; the special tokens are built once those are in.
+    int h0 = 0, h1 = 0;
+    if (a.hist) {
+        h0 = a.hist_off[row];
+        h1 = a.hist_off[row + 1];
+    }
     spx_row_params p;
     if (a.params) {
         p = a.params[row];
@@ -1869,6 +1877,8 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
         p.presence_penalty = 0.0f;
         p.frequency_penalty = 0.0f;
     }
+    U32x4 first[Elt<T>::U];
+    load_step<T, B>(a, rowp, c0, c1, 0, first);
     const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr);
     if (pl.mode == kInvalid) {
         if (split == 0 && tid == 0) write_row(a, row, -1, SPX_ROW_INVALID_PARAMS, 0);
@@ -1895,7 +1905,7 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     }
     uint32_t bad = 0;
     HistIds<B> hist;
-    load_hist<B>(a, row, pl, hist, bad);
+    load_hist_ids<B>(a, pl, h0, h1, hist, bad);
     Specials sp;
     specials_at(sp, a, lds);
     sp.any = pl.pen || banned_row != nullptr;
