@@ -1529,22 +1529,30 @@ __device__ __forceinline__ void gather_append(const uint64_t * src, int n, uint6
 }
 
 // Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
-// their ids differ), reading the list as LDS broadcasts, eight entries at a time.
+// their ids differ). A short list takes T = 2, 4, 8 or 16 threads of one wave per entry, each counting over a 1/T
+// share of the list, their counts added by lane shuffles; the list is read as LDS broadcasts, eight entries at a time.
 template <int B>
 __device__ __forceinline__ void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
-    for (int i = threadIdx.x; i < n; i += B) {
-        const uint64_t e = src[i];
+    int T = 1;
+    while (T < 16 && n * T * 2 <= B) T *= 2;
+    const int share = (n + T - 1) / T;
+    const int part = (int) threadIdx.x & (T - 1);
+    const int j0 = min(n, part * share), j1 = min(n, j0 + share);
+    for (int i0 = 0; i0 < n; i0 += B / T) {
+        const int i = i0 + (int) threadIdx.x / T;
+        const uint64_t e = i < n ? src[i] : ~0ull;
         int r = 0;
-        int j = 0;
-        for (; j + 8 <= n; j += 8) {
+        int j = j0;
+        for (; j + 8 <= j1; j += 8) {
             uint64_t v[8];
 #pragma unroll
             for (int u = 0; u < 8; u++) v[u] = src[j + u];
 #pragma unroll
             for (int u = 0; u < 8; u++) r += v[u] > e ? 1 : 0;
         }
-        for (; j < n; j++) r += src[j] > e ? 1 : 0;
-        dst[r] = e;
+        for (; j < j1; j++) r += src[j] > e ? 1 : 0;
+        for (int o = 1; o < T; o <<= 1) r += __shfl_xor(r, o, kWave);
+        if (i < n && part == 0) dst[r] = e;
     }
     __syncthreads();
 }
