@@ -116,13 +116,23 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     return __longlong_as_double((long long) r);
 }
 
-// Inclusive prefix sum over the wave's lanes (Hillis-Steele with shuffles).
+// A double moved by one DPP control, each 32-bit half on its own (0.0 where no lane feeds it).
+template <int CTRL, int ROWS, bool BOUND>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const uint64_t u = (uint64_t) __double_as_longlong(v);
+    const uint32_t lo = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) u, CTRL, ROWS, 0xf, BOUND);
+    const uint32_t hi = (uint32_t) __builtin_amdgcn_update_dpp(0, (int) (uint32_t) (u >> 32), CTRL, ROWS, 0xf, BOUND);
+    return __longlong_as_double((long long) (((uint64_t) hi << 32) | lo));
+}
+// Inclusive prefix sum of doubles over the wave's lanes through DPP, in the order of wave_incl_scan_i32 (every lane
+// active).
 __device__ __forceinline__ double wave_incl_scan_f64(double v) {
-    const int l = lane_id();
-    for (int d = 1; d < kWave; d <<= 1) {
-        const double o = __shfl_up(v, d, kWave);
-        if (l >= d) v += o;
-    }
+    v += dpp_f64<0x111, 0xf, true>(v);   // row_shr:1
+    v += dpp_f64<0x112, 0xf, true>(v);   // row_shr:2
+    v += dpp_f64<0x114, 0xf, true>(v);   // row_shr:4
+    v += dpp_f64<0x118, 0xf, true>(v);   // row_shr:8
+    v += dpp_f64<0x142, 0xa, false>(v);  // row_bcast:15
+    v += dpp_f64<0x143, 0xc, false>(v);  // row_bcast:31
     return v;
 }
 // Inclusive prefix sum of ints over the wave's lanes through DPP (every lane active).
