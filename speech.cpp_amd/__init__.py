@@ -49,6 +49,9 @@ def load_library(path=LIB_PATH):
         return _lib
     if not os.path.exists(path):
         raise RuntimeError(f"the HIP sampler library is not built: {path} is missing (run make -C {HERE})")
+    # The binding hands the library torch's device buffers and streams, so both must use one HIP runtime: torch is
+    # loaded first, and the library then binds to the runtime torch brought (the same soname), not to a second copy.
+    import torch  # noqa: F401
     lib = ctypes.CDLL(path)
     p, i32, i64, vp = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_void_p
     lib.spx_sampler_create.argtypes = [ctypes.POINTER(p), i32, i32, i32, i32]

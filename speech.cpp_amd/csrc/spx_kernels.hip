@@ -1573,7 +1573,6 @@ template <typename T, int B>
 __device__ __forceinline__ void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
                                   uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
-    constexpr int V = Elt<T>::V;
     constexpr int W = B / kWave;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     Ctl * ctl = (Ctl *) (lds + a.off_ctl);
@@ -1772,7 +1771,6 @@ template <typename T, int B>
 __device__ __forceinline__ void greedy_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
                                   uint32_t bad, unsigned char * lds, const U32x4 (&first)[Elt<T>::U]) {
-    constexpr int V = Elt<T>::V;
     constexpr int W = B / kWave;
     const int tid = threadIdx.x, lane = lane_id(), wave = tid / kWave;
     Ctl * ctl = (Ctl *) (lds + a.off_ctl);
@@ -1857,7 +1855,6 @@ __device__ __forceinline__ void greedy_row(const Launch & a, int row, int split,
 template <typename T, int B>
 __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     extern __shared__ __align__(16) unsigned char lds[];
-    constexpr int V = Elt<T>::V;
     const int tid = threadIdx.x;
     int row, split;
     xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
@@ -1894,7 +1891,6 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     }
     const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
     Ctl * ctl = (Ctl *) (lds + a.off_ctl);
-    Red * red = (Red *) (lds + a.off_red);
     const bool sampling = pl.mode != kGreedy;
 
     if (tid == 0) {
