@@ -1680,21 +1680,26 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
     const int nb = min((int) nres, cap);
     const uint32_t tkey = ctl->tau_key;
     const bool complete = tkey <= order_key(-INFINITY) && !overflow;  // the threshold never left -inf
-    // The chunk's floor, by wave 0: at or above every threshold the stream had (every token at or above it is in
-    // the buffer), with at least K entries at or above it: from the bins, or the exact K-th key where the bins would
-    // leave more than the sort takes.
-    if (!complete && tid < kWave) {
-        uint32_t kk = 0;
+    // The chunk's floor: at or above every threshold the stream had (every token at or above it is in the buffer),
+    // with at least K entries at or above it: from the bins, by every wave alike (no barrier), or the exact K-th key
+    // by wave 0 where the bins would leave more than the sort takes (the same choice in every wave).
+    uint32_t kk = 0;
+    if (!complete) {
         if (ctl->bin_scale > 0.0f) {
             uint32_t held;
             const float tb = bin_bound(ctl, pl.K, held);
             if (tb > -INFINITY && held + 64u <= (uint32_t) kSortCap) kk = order_key(tb);
         }
-        if (kk == 0) kk = buffer_bound(cand, nb, pl.K);
-        if (tid == 0) ctl->kkey = kk;
+        kk = (uint32_t) __builtin_amdgcn_readfirstlane((int) kk);
+        if (kk == 0) {
+            if (tid < kWave) {
+                const uint32_t kb = buffer_bound(cand, nb, pl.K);
+                if (tid == 0) ctl->kkey = kb;
+            }
+            __syncthreads();
+            kk = ctl->kkey;
+        }
     }
-    __syncthreads();
-    const uint32_t kk = ctl->kkey;
     const uint32_t fkey = complete ? tkey : (kk > tkey ? kk : tkey);
     const uint64_t floor = (uint64_t) fkey << 32;
     const int total = gather_sort<B>(cand, nb, floor, sorted, cand, &ctl->ncomp);
