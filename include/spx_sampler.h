@@ -109,16 +109,22 @@ void spx_sampler_destroy(spx_sampler * s);
  *   d_u            rows doubles in [0, 1], the uniform() of each drawing row (unread for greedy rows)
  *   d_out_ids      rows int32: the token picked (-1 where the row status is not OK)
  *   d_out_status   rows int32: spx_row_status
- *   d_out_kept     optional (may be null): rows int32, the number of candidates the draw picked from
- *   d_out_cand_ids, d_out_cand_probs   optional (both null or both set): rows x max_out, the first
- *                  min(kept, max_out) candidates by falling logit and their weights normalized to sum 1 over the
- *                  kept candidates (the reference's Candidates, normalized as pick() normalizes them)
+ *   d_out_kept     optional (may be null): rows int32, the size of the row's Candidates (src/common/sampling.h:10-13),
+ *                  the list the draw pick()s from: the tokens kept by top-k and top-p (TRANSFORMERS, FISH), all k
+ *                  tokens of the top-k (HARU, whose top-p gives weight 0 rather than dropping), 1 for greedy rows
+ *   d_out_cand_ids, d_out_cand_weights   optional (both null or both set): rows x max_out, the first
+ *                  min(kept, max_out) tokens of the Candidates by falling logit and their weights as the reference's
+ *                  Candidates holds them: TRANSFORMERS the softmax over the top k, not normalized again after top-p
+ *                  (src/families/qwen3-tts/sampler.cpp:84-99); HARU the float32 probabilities over the top k, 0 for
+ *                  the tokens top-p zeroes (src/families/haru/sampler.cpp:44-59); FISH the exponentials relative to
+ *                  the largest logit, not normalized (src/families/drama3/sampler.cpp:48-59); greedy rows their one
+ *                  token with weight 1. Entries past the list are -1 and 0.
  */
 spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
                            const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
                            int64_t banned_stride, const spx_row_params * d_params, const double * d_u,
                            int32_t * d_out_ids, int32_t * d_out_status, int32_t * d_out_kept,
-                           int32_t * d_out_cand_ids, float * d_out_cand_probs, void * stream);
+                           int32_t * d_out_cand_ids, double * d_out_cand_weights, void * stream);
 
 /*
  * Greedy argmax of `rows` rows with a shared or per-row suppress mask: the first largest logit, NaN ignored except in

@@ -315,16 +315,17 @@ float widen_bf16(uint16_t h) {
     return f;
 }
 
-void fill_outputs(const Drawn & d, int32_t * ids, double * probs, int cap) {
-    double total = 0;
-    for (double w : d.weights) total += w;
+// The first `cap` candidates and their weights as the reference's Candidates holds them (src/common/sampling.h:10-13):
+// TRANSFORMERS normalized over the top k and not again after top-p, HARU float32 probabilities with the zeroed ones
+// kept, FISH the unnormalized exponentials; -1 and 0 past the candidates.
+void fill_outputs(const Drawn & d, int32_t * ids, double * weights, int cap) {
     for (int i = 0; i < cap; i++) {
         if (i < (int) d.tokens.size()) {
             ids[i] = d.tokens[(size_t) i];
-            probs[i] = d.weights[(size_t) i] / total;
+            weights[i] = d.weights[(size_t) i];
         } else {
             ids[i] = -1;
-            probs[i] = 0;
+            weights[i] = 0;
         }
     }
 }
@@ -393,7 +394,7 @@ int orc_fish_candidates(const float * logits, int vocab, float temperature, int 
 void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_t ld, const int32_t * hist,
                      const int32_t * hist_off, const uint32_t * banned, int64_t banned_stride,
                      const spx_row_params * params, const double * u, orc_row_report * reports, int32_t * cand_ids,
-                     double * cand_probs, int cap, int threads) {
+                     double * cand_weights, int cap, int threads) {
     auto work = [&](int begin, int end) {
         std::vector<float> row((size_t) vocab);
         std::vector<uint8_t> ban;
@@ -417,7 +418,7 @@ void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_
             const RowOut o = sample_one(row.data(), vocab, params[r], h, nh, ban_ptr, u ? u[r] : 0.0);
             reports[r] = o.report;
             if (cand_ids && cap > 0) {
-                fill_outputs(o.drawn, cand_ids + (int64_t) r * cap, cand_probs + (int64_t) r * cap, cap);
+                fill_outputs(o.drawn, cand_ids + (int64_t) r * cap, cand_weights + (int64_t) r * cap, cap);
             }
         }
     };

@@ -63,12 +63,13 @@ typedef struct orc_row_report {
 
 /*
  * The batched semantics of spx_sample_rows on host memory, row by row as the reference's callers do. `threads` > 1
- * splits the rows over that many std::threads. cand_ids/cand_probs (rows x cap) may be null.
+ * splits the rows over that many std::threads. cand_ids/cand_weights (rows x cap) may be null: the first cap
+ * candidates of each row and their weights as the reference's Candidates holds them, -1 and 0 past them.
  */
 void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_t ld, const int32_t * hist,
                      const int32_t * hist_off, const uint32_t * banned, int64_t banned_stride,
                      const spx_row_params * params, const double * u, orc_row_report * reports, int32_t * cand_ids,
-                     double * cand_probs, int cap, int threads);
+                     double * cand_weights, int cap, int threads);
 
 /*
  * The logits one row draws from after the penalty, suppression and temperature stages of its flavor (the values the

@@ -119,9 +119,10 @@ class Sampler:
             pass
 
     def sample_rows(self, logits, params, u, hist=None, hist_off=None, banned=None, banned_stride=0, out_ids=None,
-                    out_status=None, out_kept=None, out_cand_ids=None, out_cand_probs=None, stream=None):
+                    out_status=None, out_kept=None, out_cand_ids=None, out_cand_weights=None, stream=None):
         """Samples every row of `logits` (a 2-D float32 or bfloat16 device tensor, rows may be strided). `params` is a
-        device tensor holding spx_row_params records (see device_params), `u` a float64 device tensor."""
+        device tensor holding spx_row_params records (see device_params), `u` a float64 device tensor. The optional
+        candidate outputs are int32 and float64 tensors of rows x max_out."""
         import torch
         rows, vocab = logits.shape
         dtype = BF16 if logits.dtype == torch.bfloat16 else F32
@@ -137,7 +138,7 @@ class Sampler:
         self._check(self.lib.spx_sample_rows(
             self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(hist), _ptr(hist_off), _ptr(banned),
             banned_stride, _ptr(params), _ptr(u), _ptr(out_ids), _ptr(out_status), _ptr(out_kept), _ptr(out_cand_ids),
-            _ptr(out_cand_probs), ctypes.c_void_p(s)))
+            _ptr(out_cand_weights), ctypes.c_void_p(s)))
         return out_ids, out_status
 
     def argmax_rows(self, logits, banned=None, banned_stride=0, out_ids=None, stream=None):

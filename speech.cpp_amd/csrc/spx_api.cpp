@@ -35,10 +35,9 @@ spx_status hip_fail(hipError_t e, const char * what) {
 
 size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
 
-// The launch shape and the kernel's LDS layout for one call: the control block, reduction scratch, the chunk's
-// special-token words, its list of distinct history tokens, the frequency-count table (two words per entry, at
-// least twice as many entries as history ids), the candidate buffer and the sorted candidates (also the multi-pass
-// path's radix histograms).
+// The kernel's LDS layout for one call: the control block, reduction scratch, the chunk's special-token words, its
+// list of history tokens (a power of two of entries, at least max_hist), then the candidate buffer and the sorted
+// candidates (also the radix path's histograms), which the wide path's region overlays.
 size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool has_hist, bool has_ban, int max_hist) {
     using namespace spx;
     size_t off = 0;
@@ -49,18 +48,19 @@ size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool ha
     const size_t words = (size_t) (chunk + 31) / 32;
     a.off_spec = (int) off;
     if (has_hist || has_ban) off += align_up(words * 4, 16);
+    size_t cap = 1;
+    while (cap < (size_t) max_hist) cap *= 2;
+    a.own_cap = (int) cap;
     a.off_own = (int) off;
-    if (has_hist) off += align_up((size_t) max_hist * 4, 16);
-    size_t tab = 64;
-    while (tab < 2 * (size_t) max_hist) tab *= 2;
-    a.tab_mask = (int) tab - 1;
-    a.off_tab = (int) off;
-    if (has_hist) off += tab * 8;
-    a.cand_cap = 2 * block;
+    if (has_hist) off += cap * 4;
+    a.cand_cap = std::max(2 * block, kSortCap);  // also where the merge of a row's chunks sorts up to kSortCap entries
+    off = align_up(off, 16);
     a.off_cand = (int) off;
-    if (!greedy_only) off += (size_t) a.cand_cap * 8;
-    a.off_sort = (int) off;
-    if (!greedy_only) off += (size_t) kSortCap * 8;
+    a.off_sort = (int) (off + (size_t) a.cand_cap * 8);
+    if (!greedy_only) {
+        const size_t wide = block == kBlockBig ? wide_lds_bytes<kBlockBig>() : wide_lds_bytes<kBlockSmall>();
+        off = std::max((size_t) a.off_sort + (size_t) kSortCap * 8, off + wide);
+    }
     a.lds_bytes = (int) off;
     return off;
 }
@@ -101,6 +101,25 @@ spx_status check_common(spx_sampler * s, const void * logits, int dtype, int row
     return SPX_OK;
 }
 
+// The variant of the kernel for the call's logit type and work-group size.
+hipError_t launch_sampler(const spx::Launch & a, hipStream_t s) {
+    using namespace spx;
+    if (a.nwg == 0) return hipSuccess;
+    if (a.block == kBlockBig) return a.dtype == SPX_BF16 ? launch_bf16_1024(a, s) : launch_f32_1024(a, s);
+    return a.dtype == SPX_BF16 ? launch_bf16_256(a, s) : launch_f32_256(a, s);
+}
+
+// Lets every variant take `bytes` of dynamic LDS (above the 64 KiB a launch gets without asking).
+hipError_t set_lds_limits(int bytes) {
+    using namespace spx;
+    if (bytes <= 65536) return hipSuccess;
+    for (auto f : {lds_limit_f32_1024, lds_limit_bf16_1024, lds_limit_f32_256, lds_limit_bf16_256}) {
+        const hipError_t e = f(bytes);
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
+}
+
 }  // namespace
 
 extern "C" {
@@ -127,14 +146,13 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
         s->cus = cus;
-    if (max_hist > kMaxHist) {
-        delete s;
-        return fail(SPX_ERR_INVALID_ARGUMENT, "max_hist above 4096");
+    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary, in either work-group
+    // size a call may take.
+    size_t lds_max = 0;
+    for (int block : {kBlockBig, kBlockSmall}) {
+        Launch probe{};
+        lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
     }
-    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary.
-    Launch probe{};
-    const int block = max_vocab >= kBigVocab ? kBlockBig : kBlockSmall;
-    const size_t lds_max = plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist);
     if (lds_max > 160 * 1024) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
@@ -185,13 +203,13 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
                            const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
                            int64_t banned_stride, const spx_row_params * d_params, const double * d_u,
                            int32_t * d_out_ids, int32_t * d_out_status, int32_t * d_out_kept,
-                           int32_t * d_out_cand_ids, float * d_out_cand_probs, void * stream) {
+                           int32_t * d_out_cand_ids, double * d_out_cand_weights, void * stream) {
     spx_status st = check_common(s, d_logits, dtype, rows, vocab, ld, d_banned, banned_stride, d_out_ids);
     if (st != SPX_OK) return st;
     if (rows > 0 && (!d_params || !d_u)) return fail(SPX_ERR_INVALID_ARGUMENT, "null params or u");
     if ((d_hist == nullptr) != (d_hist_off == nullptr)) return fail(SPX_ERR_INVALID_ARGUMENT, "hist and hist_off go together");
-    if ((d_out_cand_ids == nullptr) != (d_out_cand_probs == nullptr))
-        return fail(SPX_ERR_INVALID_ARGUMENT, "cand_ids and cand_probs go together");
+    if ((d_out_cand_ids == nullptr) != (d_out_cand_weights == nullptr))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "cand_ids and cand_weights go together");
     if (d_out_cand_ids && s->max_out <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "the handle was created with max_out 0");
     if (rows == 0) return SPX_OK;
     spx::Launch a = s->base;
@@ -212,10 +230,10 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_status = d_out_status;
     a.out_kept = d_out_kept;
     a.out_cand_ids = d_out_cand_ids;
-    a.out_cand_probs = d_out_cand_probs;
+    a.out_cand_w = d_out_cand_weights;
     a.max_out = d_out_cand_ids ? s->max_out : 0;
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
-    hipError_t e = spx::launch_sampler(a, (hipStream_t) stream);
+    hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
 }
@@ -243,10 +261,10 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_status = nullptr;
     a.out_kept = nullptr;
     a.out_cand_ids = nullptr;
-    a.out_cand_probs = nullptr;
+    a.out_cand_w = nullptr;
     a.max_out = 0;
     plan_launch(s, a, true, false, d_banned != nullptr);
-    hipError_t e = spx::launch_sampler(a, (hipStream_t) stream);
+    hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
 }

@@ -25,8 +25,42 @@ constexpr int kMaxSplits = 4;
 constexpr int kMaxSplitsGreedy = 16;
 // LDS bytes of a chunk's control block (its counters, bins and first-step bounds).
 constexpr int kCtlBytes = 2048;
-// The largest history a handle takes: slot ranks are kept in 24 bits and the LDS must hold the slots.
-constexpr int kMaxHist = 4096;
+// The wide path's LDS (rows whose draw runs past the candidates held): NB bins of the row's quotients and room for CAP
+// gathered tokens, per work-group size.
+template <int B>
+struct WideDims;
+template <>
+struct WideDims<1024> {
+    static constexpr int NB = 2048;
+    static constexpr int CAP = 2048;
+};
+template <>
+struct WideDims<256> {
+    static constexpr int NB = 1024;
+    static constexpr int CAP = 1024;
+};
+constexpr int kWideQs = 4;  // questions: the k-th token, the top-p cut, the pick, the last kept token
+struct WideAns {            // written by the gathered token that answers a question
+    uint64_t entry, before, through;
+    uint32_t rank, found;
+};
+template <int NB, int CAP>
+struct WideMem {
+    uint32_t pre_cnt[NB + 2];   // tokens in the bins before b; [NB + 1]: every token
+    uint64_t pre_mass[NB + 2];  // their fixed-point mass
+    uint32_t seg[NB + 1];       // where the gathered tokens of bin b go (the read appends there)
+    uint32_t need[(NB + 1 + 31) / 32];
+    uint64_t ent[CAP];
+    uint64_t mass[CAP];
+    WideAns ans[kWideQs];
+    uint64_t red[16];
+    uint64_t lo_e;              // the lowest entry of the row (its last token in the order)
+    uint32_t n_gath;
+};
+template <int B>
+constexpr size_t wide_lds_bytes() {
+    return sizeof(WideMem<WideDims<B>::NB, WideDims<B>::CAP>);
+}
 
 // What a chunk of a row leaves for the last chunk of its row.
 struct Partial {
@@ -56,13 +90,13 @@ struct Launch {
     int32_t * out_status;
     int32_t * out_kept;
     int32_t * out_cand_ids;
-    float * out_cand_probs;
+    double * out_cand_w;   // the candidates' weights (rows x max_out)
     int max_out;
     int block, splits, chunk, nwg;
     int cand_cap;  // entries of a chunk's candidate buffer
-    int tab_mask;  // entries of the frequency-count table - 1 (a power of two - 1)
-    // LDS layout (byte offsets)
-    int off_ctl, off_red, off_spec, off_own, off_tab, off_cand, off_sort, lds_bytes;
+    int own_cap;   // entries of the history list: a power of two at least max_hist
+    // LDS layout (byte offsets); the wide path's region overlays the candidate buffer and the sort area at off_cand
+    int off_ctl, off_red, off_spec, off_own, off_cand, off_sort, lds_bytes;
     // workspace
     uint32_t * counters;   // [max_rows], each back to 0 after its row's last chunk
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]
@@ -75,6 +109,13 @@ struct Launch {
 #include <hip/hip_runtime.h>
 
 namespace spx {
-hipError_t launch_sampler(const Launch & a, hipStream_t s);
-hipError_t set_lds_limits(int bytes);
+// The kernel's variants (spx_k_*.hip): logits of fp32 or bf16, work-groups of 1024 or 256 threads.
+hipError_t launch_f32_1024(const Launch & a, hipStream_t s);
+hipError_t launch_bf16_1024(const Launch & a, hipStream_t s);
+hipError_t launch_f32_256(const Launch & a, hipStream_t s);
+hipError_t launch_bf16_256(const Launch & a, hipStream_t s);
+hipError_t lds_limit_f32_1024(int bytes);
+hipError_t lds_limit_bf16_1024(int bytes);
+hipError_t lds_limit_f32_256(int bytes);
+hipError_t lds_limit_bf16_256(int bytes);
 }  // namespace spx

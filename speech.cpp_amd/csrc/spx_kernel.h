@@ -1,4 +1,5 @@
-// spx_kernels.hip — the gfx950 kernel of the batched token sampler.
+// spx_kernel.h — the gfx950 kernel of the batched token sampler, included by one source file per variant (logit
+// type x work-group size), so that the variants compile in parallel.
 //
 // One launch samples a batch. Each work-group takes one chunk of one row (a row is cut into `splits` chunks when the
 // batch alone would not fill the CUs) and reads the chunk's logits once, 16 bytes per lane per load with the next
@@ -21,6 +22,8 @@
 // (exact radix selects over the whole row) in that same work-group.
 //
 // Citations are relative to the reference checkout (nyosegawa/speech.cpp 0.11.1).
+
+#pragma once
 
 #include <float.h>
 #include <hip/hip_runtime.h>
@@ -51,6 +54,7 @@ enum Flag : uint32_t {
     kNaN0 = 16u,      // the final logit of token 0 is NaN (std::max_element then answers 0)
     kNegInf = 32u,    // a final logit of a token that is not banned is -inf
     kBadHist = 64u,   // the row's history is longer than the handle was created for
+    kTempOverPos = 128u,  // a finite final logit whose quotient is +inf (the largest quotient is then not finite)
 };
 
 struct Plan {
@@ -72,7 +76,7 @@ __device__ __forceinline__ bool neutral(const spx_row_params & p) {
     return p.repetition_penalty == 1.0f && p.presence_penalty == 0.0f && p.frequency_penalty == 0.0f;
 }
 
-__device__ __forceinline__ Plan make_plan(const spx_row_params & p, int vocab, bool has_ban, bool has_hist) {
+__device__ __forceinline__ Plan make_plan(const spx_row_params & p, int vocab, bool has_ban, bool has_hist, int max_out) {
     Plan pl;
     pl.flavor = p.flavor;
     pl.top_p = p.top_p;
@@ -112,7 +116,8 @@ __device__ __forceinline__ Plan make_plan(const spx_row_params & p, int vocab, b
     pl.t = p.flavor == SPX_FLAVOR_FISH ? fmaxf(p.temperature, 1e-5f) : p.temperature;
     pl.rt = 1.0f / pl.t;
     pl.mode = k <= kKeep ? kTopK : kFull;
-    pl.K = pl.mode == kTopK ? k : kKeepFull;
+    // a row listing its candidates holds at least the max_out it lists
+    pl.K = pl.mode == kTopK ? k : max(kKeepFull, max_out);
     pl.need_s = pl.mode == kFull || p.flavor == SPX_FLAVOR_FISH;
     return pl;
 }
@@ -247,13 +252,13 @@ static_assert(sizeof(Ctl) <= kCtlBytes, "the control block outgrows its LDS");
 
 // Per 32 tokens of the chunk one word of special bits: a banned token, or a history token of a penalized row; the
 // stream masks them to -inf. The penalty stage takes the chunk's distinct history tokens (in range, not banned) from
-// a list, each once: the thread whose atomicOr set a token's bit first appends it. Rows with a frequency penalty also
-// count each token's occurrences, in an open-addressing table keyed by token.
+// a list, each once: the thread whose atomicOr set a token's bit first appends it. A row with a frequency penalty
+// lists every occurrence instead, sorted, so that each token's occurrences are one run of the list: the run's first
+// entry stands for the token and the run's length is its count.
 struct Specials {
     uint32_t * kill;
-    int32_t * own;     // the distinct history tokens of the chunk
-    uint32_t * tab;    // frequency counts: tab[2i] the key (token + 1; 0 empty), tab[2i + 1] the count
-    int tab_mask;      // table entries - 1, a power of two - 1
+    int32_t * own;     // the distinct history tokens of the chunk, or (frequency rows) all its history ids, sorted
+    int own_cap;       // entries the list has room for: a power of two
     int n_own;
     bool any;
 };
@@ -261,8 +266,7 @@ struct Specials {
 __device__ __forceinline__ void specials_at(Specials & sp, const Launch & a, unsigned char * lds) {
     sp.kill = (uint32_t *) (lds + a.off_spec);
     sp.own = (int32_t *) (lds + a.off_own);
-    sp.tab = (uint32_t *) (lds + a.off_tab);
-    sp.tab_mask = a.tab_mask;
+    sp.own_cap = a.own_cap;
     sp.n_own = 0;
 }
 
@@ -279,70 +283,45 @@ struct Elt<uint16_t> {
     static constexpr int U = 2;
 };
 
-// History ids each thread holds: thread t the row's ids t, t + B, ... (a history is at most kMaxHist ids).
-template <int B>
-struct HistIds {
-    static constexpr int R = kMaxHist / B;
-    int id[R];
-};
-
-// The row's history ids [h0, h1) of the history (-1 past the row's history).
-template <int B>
-__device__ __forceinline__ void load_hist_ids(const Launch & a, const Plan & pl, int h0, int h1, HistIds<B> & h,
-                                              uint32_t & bad) {
-#pragma unroll
-    for (int r = 0; r < HistIds<B>::R; r++) h.id[r] = -1;
+// The row's history range [h0, h1) of the concatenated ids; flags a history longer than the handle takes.
+__device__ __forceinline__ void hist_range(const Launch & a, int row, const Plan & pl, int & h0, int & h1, uint32_t & bad) {
+    h0 = h1 = 0;
     if (!pl.pen) return;
+    h0 = a.hist_off[row];
+    h1 = a.hist_off[row + 1];
     if (h1 - h0 > a.max_hist || h1 < h0) {
         bad |= kBadHist;
         h1 = h0;
     }
-#pragma unroll
-    for (int r = 0; r < HistIds<B>::R; r++) {
-        const int j = h0 + (int) threadIdx.x + r * B;
-        if (j < h1) h.id[r] = a.hist[j];
-    }
 }
 
-// The same, the row's offsets read here.
+// Sorts v[0..n) ascending in place, n a power of two, by a bitonic network over the work-group.
 template <int B>
-__device__ __forceinline__ void load_hist(const Launch & a, int row, const Plan & pl, HistIds<B> & h, uint32_t & bad) {
-    const int h0 = pl.pen ? a.hist_off[row] : 0, h1 = pl.pen ? a.hist_off[row + 1] : 0;
-    load_hist_ids<B>(a, pl, h0, h1, h, bad);
-}
-
-__device__ __forceinline__ uint32_t token_hash(int t) { return (uint32_t) t * 2654435761u; }
-
-// One occurrence of token t in the frequency table.
-__device__ __forceinline__ void count_add(const Specials & sp, int t) {
-    const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
-    for (int probe = 0; probe <= sp.tab_mask; probe++) {
-        const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
-        const uint32_t prev = atomicCAS(&sp.tab[2 * i], 0u, key);
-        if (prev == 0u || prev == key) {
-            atomicAdd(&sp.tab[2 * i + 1], 1u);
-            return;
+__device__ __forceinline__ void block_bitonic_sort(int32_t * v, int n) {
+    for (int size = 2; size <= n; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < (n >> 1); i += B) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool up = (lo & size) == 0;
+                const int32_t x = v[lo], y = v[hi];
+                if ((x > y) == up) {
+                    v[lo] = y;
+                    v[hi] = x;
+                }
+            }
         }
     }
+    __syncthreads();
 }
 
-// The occurrences of token t counted by count_add.
-__device__ __forceinline__ int count_of(const Specials & sp, int t) {
-    const uint32_t h = token_hash(t), key = (uint32_t) t + 1u;
-    for (int probe = 0; probe <= sp.tab_mask; probe++) {
-        const uint32_t i = (h + (uint32_t) probe) & (uint32_t) sp.tab_mask;
-        const uint32_t k = sp.tab[2 * i];
-        if (k == key) return (int) sp.tab[2 * i + 1];
-        if (k == 0u) return 0;
-    }
-    return 0;
-}
-
-// The chunk's special bits, its list of distinct history tokens and (frequency rows) their counts. c0 is a multiple
-// of 64, so the chunk's words are whole words of the ban mask.
+// The chunk's special bits and its list of history tokens (see Specials). c0 is a multiple of 64, so the chunk's
+// words are whole words of the ban mask. The history ids are read from memory in slabs of B, h0..h1 of the row
+// (first: this thread's id of the first slab where the caller read it already, else -1).
 template <int B>
 __device__ __forceinline__ void build_specials(Specials & sp, int c0, int c1, const Plan & pl, const uint32_t * banned_row,
-                                      const HistIds<B> & hist, uint32_t * n_own) {
+                                      const int32_t * hist, int h0, int h1, int first, uint32_t * n_own) {
     const int nw = (c1 - c0 + 31) >> 5;
     const int tid = threadIdx.x;
     for (int w = tid; w < nw; w += B) {
@@ -354,25 +333,42 @@ __device__ __forceinline__ void build_specials(Specials & sp, int c0, int c1, co
         }
         sp.kill[w] = bw;
     }
-    if (pl.counts) {
-        for (int i = tid; i <= 2 * sp.tab_mask + 1; i += B) sp.tab[i] = 0u;
-    }
     if (tid == 0) *n_own = 0u;
     __syncthreads();
-    if (pl.pen) {
-#pragma unroll
-        for (int r = 0; r < HistIds<B>::R; r++) {
-            const int t = hist.id[r];
-            if (t >= c0 && t < c1) {
-                const uint32_t bit = 1u << ((t - c0) & 31);
-                const uint32_t old = atomicOr(&sp.kill[(t - c0) >> 5], bit);
-                if (!(old & bit)) sp.own[atomicAdd(n_own, 1u)] = t;
-                if (pl.counts) count_add(sp, t);
+    if (!pl.pen) return;
+    for (int j = h0 + tid; j < h1; j += B) {
+        const int t = j == h0 + tid && first >= 0 ? first : hist[j];
+        if (t >= c0 && t < c1) {
+            const uint32_t bit = 1u << ((t - c0) & 31);
+            const bool banned = banned_row && ((banned_row[t >> 5] >> (t & 31)) & 1u);
+            const uint32_t old = atomicOr(&sp.kill[(t - c0) >> 5], bit);
+            // a banned token stays -inf whatever its history (restricted() bans after the penalty)
+            if (!banned && (pl.counts || !(old & bit))) {
+                const uint32_t at = atomicAdd(n_own, 1u);
+                if (at < (uint32_t) sp.own_cap) sp.own[at] = t;
             }
         }
-        __syncthreads();
-        sp.n_own = (int) *n_own;
     }
+    __syncthreads();
+    sp.n_own = min((int) *n_own, sp.own_cap);
+    if (pl.counts) {
+        // every occurrence listed: sort them, padded with a value above every token, so that equal ids form runs
+        for (int i = sp.n_own + tid; i < sp.own_cap; i += B) sp.own[i] = 0x7fffffff;
+        block_bitonic_sort<B>(sp.own, sp.own_cap);
+    }
+}
+
+// Entry i of the history list: the token it stands for, or -1 where it repeats the entry before (a frequency row's
+// run), with `count` the occurrences of its token.
+__device__ __forceinline__ int own_token(const Specials & sp, const Plan & pl, int i, int & count) {
+    const int t = sp.own[i];
+    count = 1;
+    if (!pl.counts) return t;
+    if (i > 0 && sp.own[i - 1] == t) return -1;
+    int j = i + 1;
+    while (j < sp.n_own && sp.own[j] == t) j++;
+    count = j - i;
+    return t;
 }
 
 template <typename T>
@@ -386,12 +382,10 @@ __device__ __forceinline__ float load_one<uint16_t>(const uint16_t * p) {
     return bf16_to_float(*p);
 }
 
-// A distinct history token's final logit: its raw logit, read again from memory, penalized.
+// A history token's final logit: its raw logit, read again from memory, penalized (count: its occurrences).
 template <typename T>
-__device__ __forceinline__ float hist_value(const Specials & sp, int t, const spx_row_params & p, const Plan & pl,
-                                   const T * rowp) {
-    const int c = pl.counts ? count_of(sp, t) : 1;
-    return penalize(load_one<T>(rowp + t), c, p);
+__device__ __forceinline__ float hist_value(int t, int count, const spx_row_params & p, const T * rowp) {
+    return penalize(load_one<T>(rowp + t), count, p);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -521,7 +515,7 @@ __device__ __forceinline__ void slow_group(const Plan & pl, SampleSt & st, float
             const float xv = load_one<T>(rowp + id_base + (k / VV) * (B * VV) + (k % VV));
             qe = div_rn(xv, pl.t, pl.rt);
             if (__builtin_isnan(qe)) fl |= kNaN;
-            else if (qe == INFINITY) fl |= xv == INFINITY ? kPosInf : kTempOver;
+            else if (qe == INFINITY) fl |= xv == INFINITY ? kPosInf : (kTempOver | kTempOverPos);
             else if (qe == -INFINITY) fl |= xv == -INFINITY ? kNegInf : kTempOver;
             else gm = fmaxf(gm, qe);
             if (__builtin_isfinite(xv)) fl |= kFinite;
@@ -982,9 +976,10 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
         const int id = ((tot.flags & kNaN0) || tot.best == 0) ? 0 : (int) entry_id(tot.best);
         if (lane == 0) write_row(a, row, id, SPX_ROW_OK, 1);
         if (a.out_cand_ids) {
+            // the one candidate of a greedy pick, weight 1 (src/families/haru/sampler.cpp:27-31)
             for (int j = lane; j < a.max_out; j += kWave) {
                 a.out_cand_ids[(int64_t) row * a.max_out + j] = j == 0 ? id : -1;
-                a.out_cand_probs[(int64_t) row * a.max_out + j] = j == 0 ? 1.0f : 0.0f;
+                a.out_cand_w[(int64_t) row * a.max_out + j] = j == 0 ? 1.0 : 0.0;
             }
         }
         return true;
@@ -1009,8 +1004,10 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
     }
     int kept = 0, pick = -1;
     bool resolved = true;
-    double outp[4] = {0.0, 0.0, 0.0, 0.0};  // the candidates' reported weights
-    int nout = 0;                           // reported candidates
+    // The candidates' weights as the reference's Candidates holds them: TRANSFORMERS normalized over the top k and not
+    // again after top-p, HARU float32 probabilities with the zeroed ones kept, FISH the unnormalized exponentials.
+    double outp[4] = {0.0, 0.0, 0.0, 0.0};
+    int nout = 0;  // candidates listed
 
     if (pl.flavor == SPX_FLAVOR_TRANSFORMERS) {
         // candidates(): double softmax over the k kept, normalized by their sum (src/families/qwen3-tts/sampler.cpp:84-87)
@@ -1063,7 +1060,7 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
             else if (!short_k) pick = keep - 1;
             else resolved = false;
             kept = short_k ? pl.k : keep;
-            for (int j = 0; j < 4; j++) outp[j] = kq[j];
+            for (int j = 0; j < 4; j++) outp[j] = q[j];
             nout = keep;
         }
     } else if (pl.flavor == SPX_FLAVOR_HARU) {
@@ -1099,10 +1096,11 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
         // Beyond the entries held the weights must be 0: a zero among them, the cumulative share only rising.
         if (!full_known && zeros == 0) resolved = false;
         if (resolved) {
-            double w[4];
+            double w[4], wd[4];
             for (int j = 0; j < 4; j++) {
                 const float x = valid[j] ? pf[idx[j]] : 0.0f;
-                w[j] = x > 0.0f ? (double) x : 0.0;
+                wd[j] = x > 0.0f ? (double) x : 0.0;
+                w[j] = wd[j];
             }
             const double ksum = wave_sum4(w);
             for (int j = 0; j < 4; j++) w[j] /= ksum;
@@ -1116,7 +1114,7 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
             else if (last_held) pick = nk - 1;
             else resolved = false;
             kept = pl.k;
-            for (int j = 0; j < 4; j++) outp[j] = w[j];
+            for (int j = 0; j < 4; j++) outp[j] = wd[j];
             nout = nk;
         }
     } else {
@@ -1146,7 +1144,7 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
             const int f2 = wave_first4(pr2);
             pick = f2 != kNone ? f2 : keep - 1;
             kept = keep;
-            for (int j = 0; j < 4; j++) outp[j] = kw[j];
+            for (int j = 0; j < 4; j++) outp[j] = idx[j] < keep ? w[j] : 0.0;
             nout = keep;
         }
     }
@@ -1157,14 +1155,14 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
             const int i = idx[j];
             if (i < nout && i < a.max_out) {
                 a.out_cand_ids[(int64_t) row * a.max_out + i] = (int32_t) entry_id(e[i]);
-                a.out_cand_probs[(int64_t) row * a.max_out + i] = (float) outp[j];
+                a.out_cand_w[(int64_t) row * a.max_out + i] = outp[j];
             }
         }
         // entries past those written above
         for (int j = min(kept, nk) + lane; j < a.max_out; j += kWave) {
             if (j >= nout) {
                 a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
-                a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
+                a.out_cand_w[(int64_t) row * a.max_out + j] = 0.0;
             }
         }
     }
@@ -1177,11 +1175,72 @@ __device__ __forceinline__ bool finish_block(const Launch & a, int row, const sp
                                     const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf,
                                     Ctl * ctl) {
     if (threadIdx.x < kWave) {
-        const bool ok = finish_wave(a, row, p, pl, tot, e, min(n, kFinishMax), complete, pf);
+        // the entries past the finishing wave's share are not seen: the list then holds less than every token
+        const bool ok = finish_wave(a, row, p, pl, tot, e, min(n, kFinishMax), complete && n <= kFinishMax, pf);
         if (threadIdx.x == 0) ctl->resolved = ok ? 1u : 0u;
     }
     __syncthreads();
     return ctl->resolved != 0;
+}
+
+// Appends the entries of src[0..n) at or above `floor` to dst (at most kSortCap), one wave at a time per 64: a ballot,
+// one atomic per wave on the LDS count, no barrier. The order among the appended is free; the caller sorts.
+template <int B>
+__device__ __forceinline__ void gather_append(const uint64_t * src, int n, uint64_t floor, uint64_t * dst, uint32_t * count) {
+    const int lane = lane_id();
+    for (int i0 = (threadIdx.x / kWave) * kWave; i0 < n; i0 += B) {
+        const int i = i0 + lane;
+        const uint64_t e = i < n ? src[i] : 0ull;
+        const bool keep = e != 0 && e >= floor;
+        const uint64_t m = ballot(keep);
+        if (!m) continue;
+        uint32_t base = 0;
+        if (lane == 0) base = atomicAdd(count, (uint32_t) __popcll(m));
+        base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
+        const uint32_t pos = base + (uint32_t) lanes_below(m);
+        if (keep && pos < (uint32_t) kSortCap) dst[pos] = e;
+    }
+}
+
+// Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
+// their ids differ). A short list takes T = 2, 4, 8 or 16 threads of one wave per entry, each counting over a 1/T
+// share of the list, their counts added by lane shuffles; the list is read as LDS broadcasts, eight entries at a time.
+template <int B>
+__device__ __forceinline__ void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
+    int T = 1;
+    while (T < 16 && n * T * 2 <= B) T *= 2;
+    const int share = (n + T - 1) / T;
+    const int part = (int) threadIdx.x & (T - 1);
+    const int j0 = min(n, part * share), j1 = min(n, j0 + share);
+    for (int i0 = 0; i0 < n; i0 += B / T) {
+        const int i = i0 + (int) threadIdx.x / T;
+        const uint64_t e = i < n ? src[i] : ~0ull;
+        int r = 0;
+        int j = j0;
+        for (; j + 8 <= j1; j += 8) {
+            uint64_t v[8];
+#pragma unroll
+            for (int u = 0; u < 8; u++) v[u] = src[j + u];
+#pragma unroll
+            for (int u = 0; u < 8; u++) r += v[u] > e ? 1 : 0;
+        }
+        for (; j < j1; j++) r += src[j] > e ? 1 : 0;
+        for (int o = 1; o < T; o <<= 1) r += __shfl_xor(r, o, kWave);
+        if (i < n && part == 0) dst[r] = e;
+    }
+    __syncthreads();
+}
+
+// The chunk's candidates at or above `floor`, gathered from buf[0..nb) and sorted into dst; returns how many there
+// are (beyond kSortCap only the count is exact).
+template <int B>
+__device__ __forceinline__ int gather_sort(const uint64_t * buf, int nb, uint64_t floor, uint64_t * tmp, uint64_t * dst,
+                                  uint32_t * count) {
+    gather_append<B>(buf, nb, floor, tmp, count);
+    __syncthreads();
+    const int total = (int) *count;
+    rank_sort<B>(tmp, min(total, kSortCap), dst);
+    return total;
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1232,9 +1291,9 @@ __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
         if (spec) {
             __syncthreads();  // the previous chunk's special tokens are read no more
             uint32_t bad = 0;
-            HistIds<B> hist;
-            load_hist<B>(a, r.row, r.pl, hist, bad);
-            build_specials<B>(r.sp, c0, c1, r.pl, r.banned_row, hist, r.n_own);
+            int h0, h1;
+            hist_range(a, r.row, r.pl, h0, h1, bad);
+            build_specials<B>(r.sp, c0, c1, r.pl, r.banned_row, a.hist, h0, h1, -1, r.n_own);
         }
         for (int i = c0 + threadIdx.x; i < c1; i += B) {
             if (spec) {
@@ -1252,8 +1311,10 @@ __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
         }
         if (r.pl.pen) {
             for (int k = threadIdx.x; k < r.sp.n_own; k += B) {
-                const int id = r.sp.own[k];
-                const float v = hist_value<T>(r.sp, id, r.p, r.pl, rowp);
+                int cnt;
+                const int id = own_token(r.sp, r.pl, k, cnt);
+                if (id < 0) continue;
+                const float v = hist_value<T>(id, cnt, r.p, rowp);
                 const float q = div_rn(v, r.pl.t, r.pl.rt);
                 f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) id), v, q, false, id);
             }
@@ -1359,7 +1420,7 @@ __device__ __forceinline__ void fallback_row(const Launch & a, int row, const sp
             else if (v == -INFINITY) fl |= kNegInf;
             else {
                 fl |= kFinite;
-                if (!__builtin_isfinite(q)) fl |= kTempOver;
+                if (!__builtin_isfinite(q)) fl |= q > 0.0f ? (kTempOver | kTempOverPos) : kTempOver;
             }
             if (id == 0 && __builtin_isnan(v)) fl |= kNaN0;
         }
@@ -1436,7 +1497,10 @@ __device__ __forceinline__ void fallback_row(const Launch & a, int row, const sp
     Select spk;
     int id = -1;
     const uint64_t utarget = (uint64_t) ((double) kept_m * u);
-    const bool hit = sel(true, utarget, true, spk) && spk.above_n + 1 < kept_n;
+    // pick()'s last: the last kept entry for TRANSFORMERS and FISH, which draw over the kept set alone; Haru's pick()
+    // runs over all k weights (those past the kept prefix weigh 0), so any entry of the kept prefix is a hit there
+    const bool found = sel(true, utarget, true, spk);
+    const bool hit = found && (fl_ == SPX_FLAVOR_HARU ? spk.above_n < kept_n : spk.above_n + 1 < kept_n);
     if (hit) {
         id = (int) entry_id(spk.entry);
     } else if (fl_ == SPX_FLAVOR_HARU) {
@@ -1452,17 +1516,605 @@ __device__ __forceinline__ void fallback_row(const Launch & a, int row, const sp
     } else {
         id = (int) entry_id(lo_e);
     }
+    const int kept_list = fl_ == SPX_FLAVOR_HARU ? pl.k : (int) kept_n;
     if (tid == 0) {
-        write_row(a, row, id, SPX_ROW_OK, fl_ == SPX_FLAVOR_HARU ? pl.k : (int) kept_n);
-        if (a.out_cand_ids) {
-            // This path reports the id and the count of the kept candidates alone.
-            for (int j = 0; j < a.max_out; j++) {
-                a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
-                a.out_cand_probs[(int64_t) row * a.max_out + j] = 0.0f;
+        write_row(a, row, id, SPX_ROW_OK, kept_list);
+        atomicAdd(a.fb_count, 1);  // rows resolved past the one-pass path since the handle was made
+    }
+    if (!a.out_cand_ids) return;
+    // The listed candidates: the entry at the list's length by a count select, then every entry at or above it
+    // gathered and sorted (at most max_out <= 256 of them).
+    const int nlist = min(kept_list, a.max_out);
+    for (int j = nlist + tid; j < a.max_out; j += B) {
+        a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
+        a.out_cand_w[(int64_t) row * a.max_out + j] = 0.0;
+    }
+    Select sl;
+    if (nlist == 0 || !sel(false, (uint64_t) nlist, false, sl)) return;
+    uint64_t * lst = (uint64_t *) (lds + a.off_cand);  // 2 x kKeep entries, before the histograms at off_sort
+    uint32_t * nl = &((Ctl *) (lds + a.off_ctl))->ncomp;
+    if (tid == 0) *nl = 0u;
+    __syncthreads();
+    fb_visit<T, B>(r, [&](uint64_t e, float, float, bool, int) {
+        if (e && e >= sl.entry) {
+            const uint32_t at = atomicAdd(nl, 1u);
+            if (at < (uint32_t) kKeep) lst[at] = e;
+        }
+    });
+    __syncthreads();
+    const int n = min((int) *nl, nlist);
+    rank_sort<B>(lst, n, lst + kKeep);
+    const double skd = (double) kmass / kFix;  // the top k's mass relative to the largest weight
+    for (int i = tid; i < n; i += B) {
+        const uint64_t e = lst[kKeep + i];
+        const float q = entry_value(e);
+        const double w = q > -INFINITY ? exp((double) q - (double) r.top) : 0.0;
+        double out;
+        if (fl_ == SPX_FLAVOR_TRANSFORMERS) out = w / skd;
+        else if (fl_ == SPX_FLAVOR_HARU) out = (uint64_t) i < kept_n ? (double) (float) (w / skd) : 0.0;
+        else out = w;
+        a.out_cand_ids[(int64_t) row * a.max_out + i] = (int32_t) entry_id(e);
+        a.out_cand_w[(int64_t) row * a.max_out + i] = out;
+    }
+}
+
+
+// ------------------------------------------------------------------------------------------------------------------
+// The wide path: rows whose draw runs past the candidates held
+// ------------------------------------------------------------------------------------------------------------------
+//
+// A row whose top-k set or top-p set is larger than the buffer holds is resolved with further reads of the row in the
+// same work-group. The first builds a histogram in LDS of the row's final quotients: bins 1/64 wide below the largest
+// quotient (its last finite bin takes everything more than 32 below), plus one bin for the tokens at -inf, each with
+// its token count and the exact sum of the tokens' masses exp(q - top) in fixed point, so that the sums do not depend
+// on the order of the additions. The prefix sums of the bins then name the bin that holds each answer: the k-th token,
+// the token where the top-p rule cuts, the pick, the last kept token, the candidates listed. A read gathers the tokens
+// of those bins alone; each gathered token counts the tokens of its bin above it and their mass, which gives its rank
+// and its cumulative mass in the row's order, and the one token whose place answers a question writes itself. A
+// question whose answer depends on another's gets a range of bins from the bins of that one, so that usually one
+// gathering read answers all; where the bins of the exact questions alone hold more tokens than LDS takes, the row
+// goes to the radix path.
+
+// Bins per unit of quotient (a power of two, so that the bin of a quotient is exact).
+constexpr float kWideScale = 64.0f;
+
+// exp(q - top) * 2^shift rounded to an integer, 0 for q = -inf: the exponent's integer part split off exactly in double,
+// the fraction raised by one float exp2 (relative error about 1e-7).
+__device__ __forceinline__ uint64_t fixed_mass(float q, float top, int shift) {
+    if (!(q > -INFINITY)) return 0;
+    const double a = ((double) q - (double) top) * 1.4426950408889634074;
+    if (!(a > -(double) (shift + 2))) return 0;  // below 2^-2 of a unit: rounds to 0
+    const double n = __builtin_floor(a);
+    const float f = (float) (a - n);
+    const double v = __builtin_ldexp((double) __builtin_amdgcn_exp2f(f), shift + (int) n);
+    return (uint64_t) (v + 0.5);
+}
+
+// The bin of a finite quotient q <= top: the distance below the top in 1/64 units, the last finite bin beyond.
+template <int NB>
+__device__ __forceinline__ int wide_bin(float q, float top) {
+    const float d = (top - q) * kWideScale;
+    return d < (float) (NB - 1) ? (int) d : NB - 1;
+}
+
+// Exclusive prefix sum of one 64-bit value per thread over the work-group; `total` gets the sum. red: LDS of B/64.
+template <int B>
+__device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t * red, uint64_t & total) {
+    const int lane = lane_id(), wave = threadIdx.x / kWave;
+    uint64_t inc = v;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+        const uint64_t t = __shfl_up(inc, (unsigned) o, kWave);
+        if (lane >= o) inc += t;
+    }
+    if (lane == kWave - 1) red[wave] = inc;
+    __syncthreads();
+    uint64_t base = 0, tot = 0;
+    for (int w = 0; w < B / kWave; w++) {
+        const uint64_t x = red[w];
+        if (w < wave) base += x;
+        tot += x;
+    }
+    __syncthreads();
+    total = tot;
+    return base + inc - v;
+}
+
+// A question the wide path answers: the token at a rank, or the first token whose cumulative mass reaches a target
+// (GE: >=) or passes it (GT: >). lo..hi: the target or the range it lies in while it depends on another answer.
+enum WideKind : int { kQNone = 0, kQRank = 1, kQGe = 2, kQGt = 3 };
+struct WideQ {
+    int kind;
+    bool exact;       // the target is known
+    bool done;
+    uint64_t lo, hi;  // target (rank, or fixed-point mass), lo == hi when exact
+    // the answer
+    uint64_t entry;
+    uint64_t before, through;  // cumulative mass of the tokens above it, and with it
+    uint32_t rank;
+};
+enum WideQIdx : int { kQK = 0, kQCut = 1, kQPick = 2, kQLast = 3 };
+
+// The first bin whose tokens bring the cumulative count past `rank` (pre_cnt[b] <= rank < pre_cnt[b + 1]).
+template <int NB>
+__device__ __forceinline__ int bin_of_rank(const uint32_t * pre_cnt, uint64_t rank) {
+    int lo = 0, hi = NB;  // pre_cnt[0] = 0 <= rank < pre_cnt[NB + 1]
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if ((uint64_t) pre_cnt[mid] <= rank) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+// The bin holding the first token whose cumulative mass reaches x (ge) or passes it (gt); NB + 1 when none does.
+template <int NB>
+__device__ __forceinline__ int bin_of_mass(const uint64_t * pre_mass, uint64_t x, bool gt) {
+    // the first b with pre_mass[b + 1] >= x (ge) or > x (gt)
+    int lo = 0, hi = NB + 1;
+    while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        const uint64_t c = pre_mass[mid + 1];
+        if (gt ? c > x : c >= x) hi = mid;
+        else lo = mid + 1;
+    }
+    return lo;
+}
+
+// The bins a question reads: its target's bin, or the bins its target range spans (lo..hi inclusive; hi < lo: none).
+template <int NB>
+__device__ __forceinline__ void question_bins(const WideQ & q, const uint32_t * pre_cnt, const uint64_t * pre_mass,
+                                              int & b0, int & b1) {
+    b0 = 1;
+    b1 = 0;
+    if (q.kind == kQNone || q.done) return;
+    if (q.kind == kQRank) {
+        b0 = bin_of_rank<NB>(pre_cnt, q.lo);
+        b1 = bin_of_rank<NB>(pre_cnt, q.hi);
+    } else {
+        const bool gt = q.kind == kQGt;
+        b0 = bin_of_mass<NB>(pre_mass, q.lo, gt);
+        b1 = min(bin_of_mass<NB>(pre_mass, q.hi, gt), NB);
+    }
+}
+
+// The row's answers from its histogram and at most a few gathering reads. Returns false when a question's bins hold
+// more tokens than LDS takes (the caller then takes the radix path).
+template <typename T, int B>
+__device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl, float top,
+                                         unsigned char * lds) {
+    constexpr int NB = WideDims<B>::NB, CAP = WideDims<B>::CAP;
+    using Mem = WideMem<NB, CAP>;
+    Mem & m = *(Mem *) (lds + a.off_cand);
+    const int tid = threadIdx.x;
+    const int shift = 62 - (a.vocab > 1 ? 32 - __builtin_clz((uint32_t) (a.vocab - 1)) : 0);
+    FbRow r;
+    r.a = &a;
+    r.row = row;
+    r.p = p;
+    r.pl = pl;
+    r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
+    specials_at(r.sp, a, lds);
+    r.sp.any = pl.pen || r.banned_row;
+    r.top = top;
+    r.red = (Red *) (lds + a.off_red);
+    r.n_own = &((Ctl *) (lds + a.off_ctl))->n_own;
+
+    // The histogram: counts in pre_cnt, masses in pre_mass (made prefix sums below).
+    for (int i = tid; i < NB + 2; i += B) {
+        m.pre_cnt[i] = 0;
+        m.pre_mass[i] = 0;
+    }
+    if (tid == 0) m.lo_e = ~0ull;
+    __syncthreads();
+    uint64_t lo_e = ~0ull;
+    fb_visit<T, B>(r, [&](uint64_t e, float, float q, bool banned, int) {
+        if (!e) return;  // NaN: none in a row that reaches here
+        lo_e = e < lo_e ? e : lo_e;
+        if (banned || !(q > -INFINITY)) {
+            atomicAdd(&m.pre_cnt[NB], 1u);
+            return;
+        }
+        const int b = wide_bin<NB>(q, top);
+        atomicAdd(&m.pre_cnt[b], 1u);
+        const uint64_t fm = fixed_mass(q, top, shift);
+        if (fm) atomicAdd((unsigned long long *) &m.pre_mass[b], (unsigned long long) fm);
+    });
+    lo_e = wave_min_u64(lo_e);
+    if (lane_id() == 0) atomicMin((unsigned long long *) &m.lo_e, (unsigned long long) lo_e);
+    __syncthreads();
+    // prefix sums over the NB + 1 bins, each thread a contiguous run of them
+    {
+        constexpr int P = (NB + 1 + B - 1) / B;
+        const int b0 = min(tid * P, NB + 1), b1 = min(b0 + P, NB + 1);
+        uint32_t c = 0;
+        uint64_t s = 0;
+        for (int b = b0; b < b1; b++) {
+            c += m.pre_cnt[b];
+            s += m.pre_mass[b];
+        }
+        int ctot;
+        uint64_t stot;
+        const int cb = block_excl_scan_i32<B>((int) c, r.red->i, ctot);
+        const uint64_t sb = block_excl_scan_u64<B>(s, m.red, stot);
+        uint32_t cr = (uint32_t) cb;
+        uint64_t sr = sb;
+        uint32_t cnt[P];
+        uint64_t ms[P];
+        for (int j = 0; j < P; j++) {
+            const int b = b0 + j;
+            cnt[j] = b < b1 ? m.pre_cnt[b] : 0u;
+            ms[j] = b < b1 ? m.pre_mass[b] : 0ull;
+        }
+        __syncthreads();
+        for (int j = 0; j < P; j++) {
+            const int b = b0 + j;
+            if (b < b1) {
+                m.pre_cnt[b] = cr;
+                m.pre_mass[b] = sr;
+                cr += cnt[j];
+                sr += ms[j];
             }
         }
-        atomicAdd(a.fb_count, 1);  // rows this path has resolved since the handle was made
+        if (tid == 0) {
+            m.pre_cnt[NB + 1] = (uint32_t) ctot;
+            m.pre_mass[NB + 1] = stot;
+        }
+        __syncthreads();
     }
+    const uint64_t total = m.pre_mass[NB + 1];
+    const uint64_t lowest = m.lo_e;
+
+    // The questions of the row's flavor (the rules of src/families/qwen3-tts/sampler.cpp:77-99,
+    // src/families/haru/sampler.cpp:36-59, src/families/drama3/sampler.cpp:44-59 and src/common/sampling.cpp:9-19).
+    const int fl = pl.flavor;
+    const uint64_t k = (uint64_t) pl.k;
+    const double u = a.u[row];
+    WideQ q[kWideQs];
+    for (int i = 0; i < kWideQs; i++) {
+        q[i].kind = kQNone;
+        q[i].exact = true;
+        q[i].done = false;
+        q[i].lo = q[i].hi = 0;
+    }
+    const bool has_k = k < (uint64_t) a.vocab;
+    if (has_k) {
+        q[kQK].kind = kQRank;
+        q[kQK].lo = q[kQK].hi = k - 1;
+    }
+    const bool cut_tf = (fl == SPX_FLAVOR_TRANSFORMERS && pl.top_p < 1.0f) ||
+                        (fl == SPX_FLAVOR_HARU && pl.top_p > 0.0f && pl.top_p < 1.0f);
+    const bool cut_fish = fl == SPX_FLAVOR_FISH;
+    if (cut_tf || cut_fish) q[kQCut].kind = cut_tf ? kQGe : kQGt;
+    q[kQPick].kind = kQGt;
+    // What is known so far of the top-k mass, the kept count and the kept mass.
+    uint64_t sk_lo = total, sk_hi = total;  // mass of the top k
+    bool sk_known = !has_k;
+    uint64_t kept_n = k, km_lo = total, km_hi = total;
+    bool kept_known = false;
+    bool pick_fell = false;  // the pick passed no kept token before the last: it is the last kept token
+
+    auto ceil_mul = [](double f, uint64_t x) { return (uint64_t) __builtin_ceil(f * (double) x); };
+    auto floor_mul = [](double f, uint64_t x) { return (uint64_t) __builtin_floor(f * (double) x); };
+
+    // Refreshes the targets of the questions from what is known.
+    auto targets = [&]() {
+        if (has_k && q[kQK].done) {
+            sk_lo = sk_hi = q[kQK].through;
+            sk_known = true;
+        } else if (has_k) {
+            const int b = bin_of_rank<NB>(m.pre_cnt, k - 1);
+            sk_lo = m.pre_mass[b];
+            sk_hi = m.pre_mass[b + 1];
+        }
+        if (q[kQCut].kind != kQNone && !q[kQCut].done) {
+            const double tp = (double) pl.top_p;
+            if (cut_tf) {
+                q[kQCut].lo = ceil_mul(tp, sk_lo);
+                q[kQCut].hi = ceil_mul(tp, sk_hi);
+            } else {
+                q[kQCut].lo = q[kQCut].hi = floor_mul(tp, total);
+            }
+            q[kQCut].exact = q[kQCut].lo == q[kQCut].hi;
+        }
+        // the kept set
+        if (q[kQCut].kind == kQNone) {
+            kept_n = k;
+            km_lo = sk_lo;
+            km_hi = sk_hi;
+            kept_known = sk_known;
+        } else if (q[kQCut].done) {
+            const WideQ & c = q[kQCut];
+            if (cut_tf) {
+                // transformers keeps the token reaching top_p; Haru zeroes every token after it
+                kept_n = (uint64_t) c.rank + 1;
+                km_lo = km_hi = c.through;
+                kept_known = true;
+            } else if (c.rank == ~0u || (uint64_t) c.rank >= k) {
+                // fish-speech: no token of the top k passes top_p, all k are kept
+                kept_n = k;
+                km_lo = sk_lo;
+                km_hi = sk_hi;
+                kept_known = sk_known;
+            } else {
+                // fish-speech drops the token passing top_p; the first token always stays
+                kept_n = c.rank >= 1 ? (uint64_t) c.rank : 1;
+                km_lo = km_hi = c.rank >= 1 ? c.before : c.through;
+                kept_known = true;
+            }
+        } else {
+            // the cut's bins bound the kept mass
+            int b0, b1;
+            question_bins<NB>(q[kQCut], m.pre_cnt, m.pre_mass, b0, b1);
+            km_lo = m.pre_mass[min(b0, NB + 1)];
+            km_hi = m.pre_mass[min(b1 + 1, NB + 1)];
+            if (cut_fish) km_hi = max(km_hi, sk_hi);
+        }
+        if (!q[kQPick].done) {
+            q[kQPick].lo = floor_mul(u, km_lo);
+            q[kQPick].hi = floor_mul(u, km_hi);
+            q[kQPick].exact = kept_known;
+        }
+    };
+
+    // Whether every bin question i reads is among those gathered.
+    auto gathered = [&](int i) {
+        int b0, b1;
+        question_bins<NB>(q[i], m.pre_cnt, m.pre_mass, b0, b1);
+        for (int b = b0; b <= b1 && b <= NB; b++)
+            if (!((m.need[b >> 5] >> (b & 31)) & 1u)) return false;
+        return true;
+    };
+    // After an answer: the pick either hit a kept token before pick()'s last, or its answer is that last token (the
+    // k-th for Haru, whose pick() runs over all k weights; the last kept otherwise), often already known.
+    auto settle_pick = [&]() {
+        if (!q[kQPick].done || pick_fell || !kept_known) return;
+        const WideQ & P = q[kQPick];
+        const bool hit = P.rank != ~0u && (fl == SPX_FLAVOR_HARU ? (uint64_t) P.rank < kept_n
+                                                                 : (uint64_t) P.rank + 1 < kept_n);
+        if (hit) return;
+        pick_fell = true;
+        const uint64_t last = fl == SPX_FLAVOR_HARU ? k - 1 : kept_n - 1;
+        q[kQLast].kind = kQRank;
+        q[kQLast].lo = q[kQLast].hi = last;
+        q[kQLast].exact = true;
+        uint64_t known = 0;
+        if (q[kQCut].done && q[kQCut].rank != ~0u && (uint64_t) q[kQCut].rank == last) known = q[kQCut].entry;
+        else if (has_k && q[kQK].done && last == k - 1) known = q[kQK].entry;
+        else if (last + 1 == (uint64_t) a.vocab) known = lowest;
+        if (known) {
+            q[kQLast].done = true;
+            q[kQLast].entry = known;
+        }
+    };
+
+    // Gathering reads until every question is answered: each read takes the bins of the questions whose targets are
+    // known, and while they fit those of the others' target ranges; the tokens it gathers then answer every question
+    // whose target becomes known and whose bins they cover.
+    constexpr int TPT = CAP / B;  // gathered tokens per thread
+    for (int round = 0; round < 6; round++) {
+        targets();
+        bool open = false;
+        for (int i = 0; i < kWideQs; i++) open = open || (q[i].kind != kQNone && !q[i].done);
+        if (!open) break;
+        for (int i = tid; i < (NB + 1 + 31) / 32; i += B) m.need[i] = 0u;
+        __syncthreads();
+        uint32_t want = 0;
+        for (int pass = 0; pass < 2; pass++) {
+            for (int i = 0; i < kWideQs; i++) {
+                if (q[i].kind == kQNone || q[i].done || q[i].exact != (pass == 0)) continue;
+                int b0, b1;
+                question_bins<NB>(q[i], m.pre_cnt, m.pre_mass, b0, b1);
+                uint32_t add = 0;
+                for (int b = b0; b <= b1 && b <= NB; b++)
+                    if (!((m.need[b >> 5] >> (b & 31)) & 1u)) add += m.pre_cnt[b + 1] - m.pre_cnt[b];
+                if (want + add > (uint32_t) CAP) {
+                    if (pass == 0) return false;  // the bins of the known targets alone hold more than LDS takes
+                    continue;
+                }
+                want += add;
+                __syncthreads();
+                if (tid == 0)
+                    for (int b = b0; b <= b1 && b <= NB; b++) m.need[b >> 5] |= 1u << (b & 31);
+                __syncthreads();
+            }
+        }
+        // the segments of the gathered bins, in bin order
+        {
+            constexpr int P = (NB + 1 + B - 1) / B;
+            const int b0 = min(tid * P, NB + 1), b1 = min(b0 + P, NB + 1);
+            int c = 0;
+            for (int b = b0; b < b1; b++)
+                if ((m.need[b >> 5] >> (b & 31)) & 1u) c += (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
+            int tot;
+            int off = block_excl_scan_i32<B>(c, r.red->i, tot);
+            for (int b = b0; b < b1; b++) {
+                m.seg[b] = (uint32_t) off;
+                if ((m.need[b >> 5] >> (b & 31)) & 1u) off += (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
+            }
+            if (tid == 0) m.n_gath = (uint32_t) tot;
+            __syncthreads();
+        }
+        // the gathering read: each token of a needed bin appended to its bin's segment with its mass
+        fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
+            if (!e) return;
+            const bool ninf = banned || !(qq > -INFINITY);
+            const int b = ninf ? NB : wide_bin<NB>(qq, top);
+            if (!((m.need[b >> 5] >> (b & 31)) & 1u)) return;
+            const uint32_t pos = atomicAdd(&m.seg[b], 1u);
+            m.ent[pos] = e;
+            m.mass[pos] = ninf ? 0ull : fixed_mass(qq, top, shift);
+        });
+        __syncthreads();
+        // each gathered token's rank and cumulative masses, from the tokens of its bin above it, kept in registers
+        const int ng = (int) m.n_gath;
+        uint64_t te[TPT], tbefore[TPT], tthrough[TPT], trank[TPT];
+#pragma unroll
+        for (int x = 0; x < TPT; x++) {
+            const int i = tid + x * B;
+            te[x] = 0;
+            trank[x] = ~0ull;
+            tbefore[x] = tthrough[x] = 0;
+            if (i >= ng) continue;
+            const uint64_t e = m.ent[i];
+            const float qq = entry_value(e);
+            const int b = !(qq > -INFINITY) ? NB : wide_bin<NB>(qq, top);
+            const int s1 = (int) m.seg[b], s0 = s1 - (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
+            uint32_t rho = 0;
+            uint64_t mu = 0;
+            for (int j = s0; j < s1; j++) {
+                const uint64_t f = m.ent[j];
+                if (f > e) {
+                    rho++;
+                    mu += m.mass[j];
+                }
+            }
+            te[x] = e;
+            trank[x] = (uint64_t) m.pre_cnt[b] + rho;
+            tbefore[x] = m.pre_mass[b] + mu;
+            tthrough[x] = tbefore[x] + m.mass[i];
+        }
+        // answer every question the gathered tokens can, as long as answers make more targets known
+        for (int step = 0; step < kWideQs + 1; step++) {
+            bool ask[kWideQs];
+            bool any = false;
+            for (int t = 0; t < kWideQs; t++) {
+                ask[t] = q[t].kind != kQNone && !q[t].done && q[t].exact && gathered(t);
+                any = any || ask[t];
+            }
+            if (!any) break;
+            for (int t = tid; t < kWideQs; t += B) m.ans[t].found = 0u;
+            __syncthreads();
+#pragma unroll
+            for (int x = 0; x < TPT; x++) {
+                if (trank[x] == ~0ull) continue;
+                for (int t = 0; t < kWideQs; t++) {
+                    if (!ask[t]) continue;
+                    const WideQ & Q = q[t];
+                    bool hit;
+                    if (Q.kind == kQRank) hit = trank[x] == Q.lo;
+                    else if (Q.kind == kQGe) hit = Q.lo == 0 ? trank[x] == 0 : (tbefore[x] < Q.lo && Q.lo <= tthrough[x]);
+                    else hit = tbefore[x] <= Q.lo && Q.lo < tthrough[x];
+                    if (hit) {
+                        m.ans[t].entry = te[x];
+                        m.ans[t].before = tbefore[x];
+                        m.ans[t].through = tthrough[x];
+                        m.ans[t].rank = (uint32_t) trank[x];
+                        m.ans[t].found = 1u;
+                    }
+                }
+            }
+            __syncthreads();
+            for (int t = 0; t < kWideQs; t++) {
+                if (!ask[t]) continue;
+                WideQ & Q = q[t];
+                Q.done = true;
+                if (m.ans[t].found) {
+                    Q.entry = m.ans[t].entry;
+                    Q.before = m.ans[t].before;
+                    Q.through = m.ans[t].through;
+                    Q.rank = m.ans[t].rank;
+                } else {
+                    // no token reaches the target
+                    Q.entry = 0;
+                    Q.before = Q.through = total;
+                    Q.rank = ~0u;
+                }
+            }
+            __syncthreads();
+            targets();
+            settle_pick();
+        }
+        settle_pick();
+    }
+    for (int i = 0; i < kWideQs; i++)
+        if (q[i].kind != kQNone && !q[i].done) return false;
+    const uint64_t pick_e = pick_fell ? q[kQLast].entry : q[kQPick].entry;
+    const int kept_out = fl == SPX_FLAVOR_HARU ? (int) k : (int) kept_n;
+    if (tid == 0) {
+        write_row(a, row, (int) entry_id(pick_e), SPX_ROW_OK, kept_out);
+        atomicAdd(a.fb_count, 1);  // rows resolved past the one-pass path since the handle was made
+    }
+    if (!a.out_cand_ids) return true;
+
+    // The listed candidates: the first min(list, max_out) tokens of the order, gathered by one more read.
+    const uint64_t nlist = min((uint64_t) kept_out, (uint64_t) a.max_out);
+    const double sk = __builtin_ldexp((double) (has_k ? q[kQK].through : total), -shift);  // the top k's mass
+    for (int j = (int) nlist + tid; j < a.max_out; j += B) {
+        a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
+        a.out_cand_w[(int64_t) row * a.max_out + j] = 0.0;
+    }
+    if (nlist == 0) return true;
+    const int bl = bin_of_rank<NB>(m.pre_cnt, nlist - 1);
+    if (m.pre_cnt[bl + 1] > (uint32_t) CAP) return false;
+    for (int i = tid; i < (NB + 1 + 31) / 32; i += B) m.need[i] = 0u;
+    __syncthreads();
+    for (int b = tid; b <= bl; b += B) atomicOr(&m.need[b >> 5], 1u << (b & 31));
+    for (int b = tid; b <= NB; b += B) m.seg[b] = b <= bl ? m.pre_cnt[b] : 0u;
+    __syncthreads();
+    fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
+        if (!e) return;
+        const bool ninf = banned || !(qq > -INFINITY);
+        const int b = ninf ? NB : wide_bin<NB>(qq, top);
+        if (b > bl) return;
+        const uint32_t pos = atomicAdd(&m.seg[b], 1u);
+        m.ent[pos] = e;
+    });
+    __syncthreads();
+    const int ng = (int) m.pre_cnt[bl + 1];
+    for (int i = tid; i < ng; i += B) {
+        const uint64_t e = m.ent[i];
+        const float qq = entry_value(e);
+        const bool ninf = !(qq > -INFINITY);
+        const int b = ninf ? NB : wide_bin<NB>(qq, top);
+        const int s0 = (int) m.pre_cnt[b], s1 = (int) m.seg[b];
+        uint32_t rho = 0;
+        for (int j = s0; j < s1; j++) rho += m.ent[j] > e ? 1u : 0u;
+        const uint64_t rank = (uint64_t) s0 + rho;
+        if (rank >= nlist) continue;
+        const double w = ninf ? 0.0 : exp((double) qq - (double) top);
+        double out;
+        if (fl == SPX_FLAVOR_TRANSFORMERS) out = w / sk;
+        else if (fl == SPX_FLAVOR_HARU) out = rank < kept_n ? (double) (float) (w / sk) : 0.0;
+        else out = w;
+        a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(e);
+        a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = out;
+    }
+    return true;
+}
+
+// A row the one-pass path could not finish: its status from the stream's flags and its largest quotient, then the
+// wide path, or where the bins it needs hold more tokens than LDS takes, the radix path. `top`: the largest final
+// quotient where the one-pass path knows it (its sorted candidates' first), else NaN, and a read finds it.
+template <typename T, int B>
+__device__ __forceinline__ void resolve_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+                                            uint32_t F, float top, unsigned char * lds) {
+    if (__builtin_isnan(top)) {
+        FbRow r;
+        r.a = &a;
+        r.row = row;
+        r.p = p;
+        r.pl = pl;
+        r.banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
+        specials_at(r.sp, a, lds);
+        r.sp.any = pl.pen || r.banned_row;
+        r.top = 0.0f;
+        r.red = (Red *) (lds + a.off_red);
+        r.n_own = &((Ctl *) (lds + a.off_ctl))->n_own;
+        uint64_t hi = 0;
+        fb_visit<T, B>(r, [&](uint64_t e, float, float, bool banned, int) {
+            if (e && !banned) hi = e > hi ? e : hi;
+        });
+        hi = block_max_u64<B>(hi, r.red->u);
+        top = hi ? entry_value(hi) : -INFINITY;
+    }
+    const int st = row_status(pl, p, F, __builtin_isfinite(top) && !(F & kTempOverPos));
+    if (st >= 0) {
+        if (threadIdx.x == 0) write_row(a, row, -1, st, 0);
+        return;
+    }
+    if (wide_row<T, B>(a, row, p, pl, top, lds)) return;
+    __syncthreads();
+    fallback_row<T, B>(a, row, p, pl, F, lds);
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -1509,66 +2161,6 @@ __device__ __forceinline__ uint32_t nan0_flag(const T * rowp, const Plan & pl, c
     return __builtin_isnan(load_one<T>(rowp)) ? kNaN0 : 0u;
 }
 
-// Appends the entries of src[0..n) at or above `floor` to dst (at most kSortCap), one wave at a time per 64: a ballot,
-// one atomic per wave on the LDS count, no barrier. The order among the appended is free; the caller sorts.
-template <int B>
-__device__ __forceinline__ void gather_append(const uint64_t * src, int n, uint64_t floor, uint64_t * dst, uint32_t * count) {
-    const int lane = lane_id();
-    for (int i0 = (threadIdx.x / kWave) * kWave; i0 < n; i0 += B) {
-        const int i = i0 + lane;
-        const uint64_t e = i < n ? src[i] : 0ull;
-        const bool keep = e != 0 && e >= floor;
-        const uint64_t m = ballot(keep);
-        if (!m) continue;
-        uint32_t base = 0;
-        if (lane == 0) base = atomicAdd(count, (uint32_t) __popcll(m));
-        base = (uint32_t) __builtin_amdgcn_readfirstlane((int) base);
-        const uint32_t pos = base + (uint32_t) lanes_below(m);
-        if (keep && pos < (uint32_t) kSortCap) dst[pos] = e;
-    }
-}
-
-// Sorts src[0..n) into falling order in dst by rank: each entry counts the entries above it (entries are distinct,
-// their ids differ). A short list takes T = 2, 4, 8 or 16 threads of one wave per entry, each counting over a 1/T
-// share of the list, their counts added by lane shuffles; the list is read as LDS broadcasts, eight entries at a time.
-template <int B>
-__device__ __forceinline__ void rank_sort(const uint64_t * src, int n, uint64_t * dst) {
-    int T = 1;
-    while (T < 16 && n * T * 2 <= B) T *= 2;
-    const int share = (n + T - 1) / T;
-    const int part = (int) threadIdx.x & (T - 1);
-    const int j0 = min(n, part * share), j1 = min(n, j0 + share);
-    for (int i0 = 0; i0 < n; i0 += B / T) {
-        const int i = i0 + (int) threadIdx.x / T;
-        const uint64_t e = i < n ? src[i] : ~0ull;
-        int r = 0;
-        int j = j0;
-        for (; j + 8 <= j1; j += 8) {
-            uint64_t v[8];
-#pragma unroll
-            for (int u = 0; u < 8; u++) v[u] = src[j + u];
-#pragma unroll
-            for (int u = 0; u < 8; u++) r += v[u] > e ? 1 : 0;
-        }
-        for (; j < j1; j++) r += src[j] > e ? 1 : 0;
-        for (int o = 1; o < T; o <<= 1) r += __shfl_xor(r, o, kWave);
-        if (i < n && part == 0) dst[r] = e;
-    }
-    __syncthreads();
-}
-
-// The chunk's candidates at or above `floor`, gathered from buf[0..nb) and sorted into dst; returns how many there
-// are (beyond kSortCap only the count is exact).
-template <int B>
-__device__ __forceinline__ int gather_sort(const uint64_t * buf, int nb, uint64_t floor, uint64_t * tmp, uint64_t * dst,
-                                  uint32_t * count) {
-    gather_append<B>(buf, nb, floor, tmp, count);
-    __syncthreads();
-    const int total = (int) *count;
-    rank_sort<B>(tmp, min(total, kSortCap), dst);
-    return total;
-}
-
 template <typename T, int B>
 __device__ __forceinline__ void sample_row(const Launch & a, int row, int split, const spx_row_params & p, const Plan & pl,
                                   int c0, int c1, const T * rowp, const uint32_t * banned_row, Specials & sp,
@@ -1603,13 +2195,16 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
         const float tau = tk ? key_float(tk) : -INFINITY;
         for (int i0 = 0; i0 < sp.n_own; i0 += B) {
             const int i = i0 + tid;
-            const bool live = i < sp.n_own;
-            int hid = 0;
+            bool live = i < sp.n_own;
+            int hid = 0, cnt = 1;
             float hv = 0.0f;
             if (live) {
-                hid = sp.own[i];
+                hid = own_token(sp, pl, i, cnt);
+                live = hid >= 0;
+            }
+            if (live) {
                 const float raw = i0 == 0 ? raw0 : load_one<T>(rowp + hid);
-                hv = penalize(raw, pl.counts ? count_of(sp, hid) : 1, p);
+                hv = penalize(raw, cnt, p);
             }
             float q = -INFINITY;
             if (live && hid == 0 && __builtin_isnan(hv)) st.flags |= kNaN0;
@@ -1620,7 +2215,7 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
                 else if (hv == -INFINITY) st.flags |= kNegInf;
                 else {
                     st.flags |= kFinite;
-                    if (!__builtin_isfinite(q)) st.flags |= kTempOver;
+                    if (!__builtin_isfinite(q)) st.flags |= q > 0.0f ? (kTempOver | kTempOverPos) : kTempOver;
                 }
             }
             const bool fin = live && q > -INFINITY && q < INFINITY;
@@ -1711,8 +2306,10 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
     if (a.splits == 1) {
         RowTotals t{0ull, S, M, F};
         if (broken || !finish_block<B>(a, row, p, pl, t, cand, ntot, complete, pf, ctl)) {
+            // the largest quotient: the sorted candidates' first, unless entries were dropped
+            const float top = broken ? NAN : (ntot > 0 ? entry_value(cand[0]) : -INFINITY);
             __syncthreads();
-            fallback_row<T, B>(a, row, p, pl, F, lds);
+            resolve_row<T, B>(a, row, p, pl, F, top, lds);
         }
         return;
     }
@@ -1767,8 +2364,9 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
         rank_sort<B>(sorted, tot, cand);
     }
     if (any_broken || !finish_block<B>(a, row, p, pl, t, cand, tot, all_complete, pf, ctl)) {
+        const float top = any_broken ? NAN : (tot > 0 ? entry_value(cand[0]) : -INFINITY);
         __syncthreads();
-        fallback_row<T, B>(a, row, p, pl, t.flags, lds);
+        resolve_row<T, B>(a, row, p, pl, t.flags, top, lds);
     }
 }
 
@@ -1817,8 +2415,10 @@ __device__ __forceinline__ void greedy_row(const Launch & a, int row, int split,
         uint64_t hb = 0;
         uint32_t hf = 0;
         for (int i = tid; i < sp.n_own; i += B) {
-            const int hid = sp.own[i];
-            const float hv = hist_value<T>(sp, hid, p, pl, rowp);
+            int cnt;
+            const int hid = own_token(sp, pl, i, cnt);
+            if (hid < 0) continue;
+            const float hv = hist_value<T>(hid, cnt, p, rowp);
             if (hid == 0 && __builtin_isnan(hv)) hf |= kNaN0;
             if (__builtin_isnan(hv)) hf |= kNaN;
             else if (hv == -INFINITY) hf |= kNegInf;
@@ -1889,7 +2489,7 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     }
     U32x4 first[Elt<T>::U];
     load_step<T, B>(a, rowp, c0, c1, 0, first);
-    const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr);
+    const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr, a.max_out);
     if (pl.mode == kInvalid) {
         if (split == 0 && tid == 0) write_row(a, row, -1, SPX_ROW_INVALID_PARAMS, 0);
         return;
@@ -1913,47 +2513,33 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
         for (int i = tid; i < kBins; i += B) ctl->bins[i] = 0;
     }
     uint32_t bad = 0;
-    HistIds<B> hist;
-    load_hist_ids<B>(a, pl, h0, h1, hist, bad);
+    if (!pl.pen) h1 = h0;
+    if (h1 - h0 > a.max_hist || h1 < h0) {
+        bad |= kBadHist;
+        h1 = h0;
+    }
+    // the first slab of history ids, requested before the LDS set-up
+    const int hfirst = h0 + tid < h1 ? a.hist[h0 + tid] : -1;
     Specials sp;
     specials_at(sp, a, lds);
     sp.any = pl.pen || banned_row != nullptr;
-    if (sp.any) build_specials<B>(sp, c0, c1, pl, banned_row, hist, &ctl->n_own);
+    if (sp.any) build_specials<B>(sp, c0, c1, pl, banned_row, a.hist, h0, h1, hfirst, &ctl->n_own);
     __syncthreads();
     if (sampling) sample_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
     else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
 }
 
-// ------------------------------------------------------------------------------------------------------------------
-// Launchers
-// ------------------------------------------------------------------------------------------------------------------
-
-hipError_t launch_sampler(const Launch & a, hipStream_t s) {
-    if (a.nwg == 0) return hipSuccess;
-    if (a.block == kBlockBig) {
-        if (a.dtype == SPX_BF16)
-            hipLaunchKernelGGL((sampler_kernel<uint16_t, kBlockBig>), dim3(a.nwg), dim3(kBlockBig), a.lds_bytes, s, a);
-        else
-            hipLaunchKernelGGL((sampler_kernel<float, kBlockBig>), dim3(a.nwg), dim3(kBlockBig), a.lds_bytes, s, a);
-    } else {
-        if (a.dtype == SPX_BF16)
-            hipLaunchKernelGGL((sampler_kernel<uint16_t, kBlockSmall>), dim3(a.nwg), dim3(kBlockSmall), a.lds_bytes, s, a);
-        else
-            hipLaunchKernelGGL((sampler_kernel<float, kBlockSmall>), dim3(a.nwg), dim3(kBlockSmall), a.lds_bytes, s, a);
-    }
-    return hipGetLastError();
-}
-
-hipError_t set_lds_limits(int bytes) {
-    if (bytes <= 65536) return hipSuccess;
-    const void * fns[4] = {(const void *) sampler_kernel<float, kBlockBig>, (const void *) sampler_kernel<uint16_t, kBlockBig>,
-                           (const void *) sampler_kernel<float, kBlockSmall>,
-                           (const void *) sampler_kernel<uint16_t, kBlockSmall>};
-    for (const void * f : fns) {
-        const hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-        if (e != hipSuccess) return e;
-    }
-    return hipSuccess;
-}
-
 }  // namespace spx
+
+// One variant of the kernel: its launcher and its LDS limit, named spx::launch_<NAME> and spx::lds_limit_<NAME>.
+#define SPX_KERNEL_VARIANT(T, B, NAME)                                                                          \
+    namespace spx {                                                                                             \
+    hipError_t launch_##NAME(const Launch & a, hipStream_t s) {                                                 \
+        hipLaunchKernelGGL((sampler_kernel<T, B>), dim3(a.nwg), dim3(B), a.lds_bytes, s, a);                    \
+        return hipGetLastError();                                                                               \
+    }                                                                                                           \
+    hipError_t lds_limit_##NAME(int bytes) {                                                                    \
+        return hipFuncSetAttribute((const void *) sampler_kernel<T, B>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+                                   bytes);                                                                      \
+    }                                                                                                           \
+    }

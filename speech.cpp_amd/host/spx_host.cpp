@@ -50,7 +50,7 @@ public:
         check_spx(spx_sampler_create(&handle_, 1, vocab, hist, listed_));
         const size_t words = (size_t) (vocab + 31) / 32;
         const size_t bytes = (size_t) vocab * 4 + sizeof(spx_row_params) + 8 + (size_t) std::max(hist, 1) * 4 + 8 +
-                             words * 4 + 3 * 4 + (size_t) listed_ * 8 + 64;
+                             words * 4 + 3 * 4 + (size_t) listed_ * 12 + 64;
         check_hip(hipMalloc(&base_, bytes), "hipMalloc");
         char * p = (char *) base_;
         auto take = [&](size_t n) { void * r = p; p += (n + 15) / 16 * 16; return r; };
@@ -62,7 +62,7 @@ public:
         banned_ = (uint32_t *) take(words * 4);
         out_ = (int32_t *) take(3 * 4);
         cand_ids_ = (int32_t *) take((size_t) listed_ * 4);
-        cand_probs_ = (float *) take((size_t) listed_ * 4);
+        cand_w_ = (double *) take((size_t) listed_ * 8);
         check_hip(hipStreamCreateWithFlags(&stream_, hipStreamNonBlocking), "hipStreamCreate");
     }
     ~Workspace() {
@@ -78,7 +78,7 @@ public:
     struct Row {
         int32_t id, status, kept;
         std::vector<int32_t> ids;
-        std::vector<float> probs;
+        std::vector<double> weights;
     };
 
     Row run(const std::vector<float> & logits, const spx_row_params & p, const std::vector<int32_t> * history,
@@ -113,16 +113,16 @@ public:
         }
         check_spx(spx_sample_rows(handle_, logits_, SPX_F32, 1, vocab, vocab, d_hist, d_hist_off, d_banned, 0, params_, u_,
                                   out_, out_ + 1, out_ + 2, want_candidates ? cand_ids_ : nullptr,
-                                  want_candidates ? cand_probs_ : nullptr, stream_));
+                                  want_candidates ? cand_w_ : nullptr, stream_));
         int32_t o[3];
         check_hip(hipMemcpyAsync(o, out_, sizeof o, hipMemcpyDeviceToHost, stream_), "copy result");
         Row r;
         if (want_candidates) {
             r.ids.resize((size_t) listed_);
-            r.probs.resize((size_t) listed_);
+            r.weights.resize((size_t) listed_);
             check_hip(hipMemcpyAsync(r.ids.data(), cand_ids_, (size_t) listed_ * 4, hipMemcpyDeviceToHost, stream_),
                       "copy ids");
-            check_hip(hipMemcpyAsync(r.probs.data(), cand_probs_, (size_t) listed_ * 4, hipMemcpyDeviceToHost, stream_),
+            check_hip(hipMemcpyAsync(r.weights.data(), cand_w_, (size_t) listed_ * 8, hipMemcpyDeviceToHost, stream_),
                       "copy weights");
         }
         check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
@@ -144,7 +144,7 @@ private:
     uint32_t * banned_ = nullptr;
     int32_t * out_ = nullptr;
     int32_t * cand_ids_ = nullptr;
-    float * cand_probs_ = nullptr;
+    double * cand_w_ = nullptr;
     hipStream_t stream_ = nullptr;
     std::vector<int32_t> staged_off_;
     std::vector<uint32_t> staged_bits_;
@@ -220,7 +220,7 @@ Candidates to_candidates(const Workspace::Row & r) {
             throw Error(Fault::InvalidArgument, "the draw keeps " + std::to_string(r.kept) +
                                                     " tokens, more than the device lists; sample() draws from them");
         c.tokens.push_back(r.ids[(size_t) i]);
-        c.weights.push_back((double) r.probs[(size_t) i]);
+        c.weights.push_back(r.weights[(size_t) i]);
     }
     return c;
 }

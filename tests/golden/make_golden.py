@@ -6,7 +6,8 @@ reference_sampling.npz: the outputs of the reference's own src/common/sampling.c
     wherever the reference is absent.
 workloads.npz: per workload of tests/workloads.py at a reduced row count, the digest of the seeded inputs and the
     oracle's answer per row (id, status, kept, distance of u to the nearest boundary and of the top-p decision to
-    top_p) plus its first 8 candidates and probabilities. The GPU tests hold the HIP path to them.
+    top_p) plus its first 8 candidates and their weights (the reference's Candidates). The GPU tests hold the HIP path
+    to them.
 """
 import hashlib
 import os
@@ -66,7 +67,7 @@ def workload_fixture():
     out = {}
     for name, rows, seed in WORKLOADS:
         w = workloads.make(name, rows=rows, seed=seed)
-        reports, cids, cprobs = oracle_lib.sample_rows(w, cap=NCAND)
+        reports, cids, cweights = oracle_lib.sample_rows(w, cap=NCAND)
         out[name + "/digest"] = np.array(digest(w))
         out[name + "/rows"] = np.array(rows)
         out[name + "/seed"] = np.array(seed)
@@ -76,7 +77,7 @@ def workload_fixture():
         out[name + "/boundary"] = reports["boundary"].copy()
         out[name + "/cut"] = reports["cut"].copy()
         out[name + "/cand_ids"] = cids
-        out[name + "/cand_probs"] = cprobs
+        out[name + "/cand_weights"] = cweights
     np.savez(os.path.join(HERE, "workloads.npz"), **out)
     print("wrote workloads.npz")
 

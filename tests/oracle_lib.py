@@ -123,14 +123,15 @@ def final_logits(logits, params, hist=None, banned=None):
 
 
 def sample_rows(w, threads=8, cap=0):
-    """The oracle over a tests.workloads.Workload: per-row reports, and the first `cap` candidates and probabilities."""
+    """The oracle over a tests.workloads.Workload: per-row reports, and the first `cap` candidates and their weights
+    (the reference's Candidates.weights)."""
     rows, vocab = w["logits"].shape
     reports = np.zeros(rows, dtype=REPORT)
     cids = np.zeros((rows, cap), dtype=np.int32) if cap else None
-    cprobs = np.zeros((rows, cap), dtype=np.float64) if cap else None
+    cweights = np.zeros((rows, cap), dtype=np.float64) if cap else None
     logits = np.ascontiguousarray(w["logits"])
     dtype = 1 if w["dtype"] == "bf16" else 0
     oracle().orc_sample_rows(_ptr(logits), dtype, rows, vocab, vocab, _ptr(w["hist"]), _ptr(w["hist_off"]),
                              _ptr(w["banned"]), w["banned_stride"], _ptr(np.ascontiguousarray(w["params"])),
-                             _ptr(w["u"]), _ptr(reports), _ptr(cids), _ptr(cprobs), cap, threads)
-    return reports, cids, cprobs
+                             _ptr(w["u"]), _ptr(reports), _ptr(cids), _ptr(cweights), cap, threads)
+    return reports, cids, cweights

@@ -45,11 +45,11 @@ def test_workload_inputs_regenerate(name, rows, seed):
 def test_oracle_reproduces_the_workload_answers(name, rows, seed):
     g = load("workloads.npz")
     w = workloads.make(name, rows=rows, seed=seed)
-    reports, cids, cprobs = oracle_lib.sample_rows(w, cap=NCAND)
+    reports, cids, cweights = oracle_lib.sample_rows(w, cap=NCAND)
     for key in ("id", "status", "kept", "boundary", "cut"):
         np.testing.assert_array_equal(reports[key], g[name + "/" + key], err_msg=key)
     np.testing.assert_array_equal(cids, g[name + "/cand_ids"])
-    np.testing.assert_array_equal(cprobs, g[name + "/cand_probs"])
+    np.testing.assert_array_equal(cweights, g[name + "/cand_weights"])
 
 
 @pytest.mark.gpu
@@ -63,6 +63,6 @@ def test_hip_path_matches_the_workload_answers(name, rows, seed):
     spx = workloads.spx_module()
     sampler = spx.Sampler(max_rows=rows, max_vocab=w.vocab, max_hist=2048, max_out=NCAND)
     gpu = gpu_harness.run_gpu(sampler, w, max_out=NCAND)
-    counts, bad = gpu_harness.compare(w, gpu, reports, g[name + "/cand_ids"], g[name + "/cand_probs"])
+    counts, bad = gpu_harness.compare(w, gpu, reports, g[name + "/cand_ids"], g[name + "/cand_weights"])
     print(name, counts)
     assert not bad, bad[:5]

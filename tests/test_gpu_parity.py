@@ -20,12 +20,18 @@ def sampler():
     return spx.Sampler(max_rows=2048, max_vocab=151936, max_hist=2048, max_out=MAX_OUT)
 
 
+# Rows a test may excuse for lying within 1e-6 of a boundary or of the top-p decision: such rows are rare (about 2e-6
+# of the draws), so more than one in a test means an error of the device larger than the excuse.
+NEAR_BUDGET = 1
+
+
 def check(sampler, w, cap=MAX_OUT, allow_explained=True):
-    reports, cids, cprobs = oracle_lib.sample_rows(w, cap=cap)
+    reports, cids, cweights = oracle_lib.sample_rows(w, cap=cap)
     gpu = gpu_harness.run_gpu(sampler, w, max_out=cap)
-    counts, bad = gpu_harness.compare(w, gpu, reports, cids, cprobs)
-    print(w["name"], counts, bad)
+    counts, bad = gpu_harness.compare(w, gpu, reports, cids, cweights)
+    print(w["name"], counts, bad[:5], flush=True)
     assert not bad, f"{len(bad)} unexplained rows, first: {bad[:5]}"
+    assert counts["boundary"] + counts["cut"] <= NEAR_BUDGET, counts
     if not allow_explained:
         assert counts["tie"] + counts["boundary"] + counts["cut"] == 0
     return counts, gpu, reports
@@ -37,6 +43,14 @@ def test_workload_parity(sampler, name, rows):
     counts, gpu, _ = check(sampler, w)
     # Explained differences are counted, not hidden: ties dominate the talker rows, whose 8 largest logits are equal.
     assert counts["same"] + counts["tie"] >= 0.95 * w.rows
+
+
+def test_mixed_full_batch(sampler):
+    # The heterogeneous batch at its own launch shape: 2048 x 151936 bf16, one row per work-group, the rows whose
+    # top-p set runs past the buffer resolved by the wide path; every row against the oracle.
+    w = workloads.make("mixed", seed=1234)
+    counts, _, _ = check(sampler, w, cap=16)
+    assert counts["same"] + counts["tie"] == w.rows - counts["boundary"] - counts["cut"]
 
 
 def test_talker_spikes_are_ties(sampler):
@@ -114,6 +128,19 @@ EDGE = [
     ("haru top-k 1000", dict(flavor=1, temperature=1.2, top_k=1000, top_p=0.9), np.random.default_rng(2).normal(0, 2, 8192), None),
     ("wide top-p fallback", dict(temperature=2.5, top_k=0, top_p=0.99), np.random.default_rng(3).normal(0, 2, 3072), None),
     ("full draw fallback", dict(temperature=3.0, top_k=0, top_p=1.0), np.random.default_rng(4).normal(0, 1, 20000), None),
+    ("haru ties", dict(flavor=1, temperature=1.0, top_k=0, top_p=1.0), [1.0, 3.0, 3.0, 2.0, 3.0], None),
+    ("haru ties top-p", dict(flavor=1, temperature=1.0, top_k=4, top_p=0.5), [1.0, 3.0, 3.0, 2.0, 3.0], None),
+    ("fish ties", dict(flavor=2, temperature=1.0, top_k=5, top_p=1.0), [1.0, 3.0, 3.0, 2.0, 3.0], None),
+    ("greedy ties", dict(greedy=True), [2.0, 2.0], None),
+    ("haru greedy ties", dict(flavor=1, temperature=0.0), [2.0, 2.0, 1.0], None),
+    ("fish greedy ties", dict(flavor=2, greedy=True), [1.0, 2.0, 2.0], None),
+    # one token reaches top_p under a top-k the buffer does not hold: Haru's pick() still runs over all k weights
+    ("haru one token past top-p, top-k 1000", dict(flavor=1, temperature=1.0, top_k=1000, top_p=0.5),
+     np.concatenate([[12.0], np.random.default_rng(5).normal(0, 1, 4095)]), None),
+    ("transformers one token past top-p, top-k 1000", dict(temperature=1.0, top_k=1000, top_p=0.5),
+     np.concatenate([[12.0], np.random.default_rng(5).normal(0, 1, 4095)]), None),
+    ("fish top-k 1000", dict(flavor=2, temperature=1.3, top_k=1000, top_p=0.95),
+     np.random.default_rng(6).normal(0, 1, 4097), None),
     ("invalid flavor", dict(flavor=7), [1.0, 2.0], None),
     ("invalid temperature", dict(temperature=0.0), [1.0, 2.0], None),
 ]
@@ -154,6 +181,35 @@ def test_flavors_mixed_batch(sampler):
     check(sampler, w)
 
 
+def test_merge_of_three_chunks_with_wide_top_k(sampler):
+    # 4 rows of 16000 tokens are cut into 3 chunks each; with top-k 256 (and 0) every chunk publishes up to 256
+    # candidates, which the row's last chunk merges and sorts.
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(14)
+    rows, vocab = 4, 16000
+    logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+    p = spx.row_params(rows, temperature=1.0, top_k=np.array([256, 256, 0, 200]), top_p=np.array([1.0, 0.9, 0.5, 1.0]))
+    w = workloads.Workload(name="merge3", logits=logits, dtype="f32", params=p, u=workloads.uniforms(15, rows),
+                           hist=None, hist_off=None, banned=None, banned_stride=0)
+    check(sampler, w)
+
+
+def test_heavy_ban_leaves_few_tokens_across_the_vocabulary(sampler):
+    # A mask that leaves about 400 tokens spread over 151936: the row is cut into chunks each holding every live
+    # token, more of them together than the finishing wave takes.
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(16)
+    rows, vocab = 4, 151936
+    logits = rng.normal(0, 1, (rows, vocab)).astype(np.float32)
+    live = rng.choice(vocab, 400, replace=False)
+    ban = np.setdiff1d(np.arange(vocab), live)
+    banned = spx.pack_bans([ban], vocab)
+    p = spx.row_params(rows, temperature=1.0, top_k=0, top_p=np.array([1.0, 0.99, 0.5, 1.0]))
+    w = workloads.Workload(name="heavy ban", logits=logits, dtype="f32", params=p, u=workloads.uniforms(17, rows),
+                           hist=None, hist_off=None, banned=banned, banned_stride=0)
+    check(sampler, w)
+
+
 def test_repeated_calls_reuse_workspace(sampler):
     # The per-row counters and the fallback list reset themselves: calls in a row give the same answers.
     w = workloads.make("mixed", rows=64, seed=21)
@@ -175,3 +231,85 @@ def test_empty_batch(sampler):
     ids, st = sampler.sample_rows(logits, p, u)
     torch.cuda.synchronize()
     assert ids.numel() == 0
+
+
+def _share_rows(name):
+    """One row of a workload shape and its settings, for the draw-share test."""
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(23)
+    if name == "talker":
+        logits = rng.normal(0.0, 2.0, 3072).astype(np.float32)
+        p = spx.row_params(1, spx.TRANSFORMERS, temperature=0.9, top_k=50, top_p=1.0)
+    elif name == "haru-shape":
+        logits = workloads.zipf_logits(rng, 1, 151936)[0]
+        p = spx.row_params(1, spx.TRANSFORMERS, temperature=0.7, top_k=0, top_p=0.9)
+    elif name == "haru-flavor":
+        logits = workloads.zipf_logits(rng, 1, 151936)[0]
+        p = spx.row_params(1, spx.HARU, temperature=0.7, top_k=25, top_p=0.9)
+    else:
+        logits = rng.normal(0.0, 2.0, 4097).astype(np.float32)
+        p = spx.row_params(1, spx.FISH, temperature=0.8, top_k=30, top_p=0.9)
+    return logits, p
+
+
+@pytest.mark.parametrize("name", ["talker", "haru-shape", "haru-flavor", "fish"])
+def test_draws_over_one_row(sampler, name):
+    # checks/qwen3-tts/qwen3-tts-graph-sampler-check.cpp:97-160 on the device: one row drawn with 64 numbers, half
+    # spread evenly over [0, 1] and half from uniform() of seed 1, each pick against the oracle's; then 25,600 draws
+    # from uniform(), whose shares must lie within five standard deviations of the candidates' probabilities, a pick
+    # of a token that is no candidate failing however rare.
+    import torch
+    logits, p = _share_rows(name)
+    vocab = len(logits)
+    rng = workloads.MT64(1)
+    u = np.array([(i + 0.5) / 32 for i in range(32)] + [rng.uniform() for _ in range(32)])
+    w = workloads.Workload(name="draws " + name, logits=np.tile(logits, (64, 1)), dtype="f32", params=np.repeat(p, 64),
+                           u=u, hist=None, hist_off=None, banned=None, banned_stride=0)
+    check(sampler, w)
+    # the shares of 25,600 draws
+    st, toks, wts = (oracle_lib.tf_candidates(logits, p[0]) if p["flavor"][0] == 0 else
+                     oracle_lib.haru_candidates(logits, float(p["temperature"][0]), int(p["top_k"][0]),
+                                                float(p["top_p"][0])) if p["flavor"][0] == 1 else
+                     oracle_lib.fish_candidates(logits, float(p["temperature"][0]), int(p["top_k"][0]),
+                                                float(p["top_p"][0])))
+    assert st == 0
+    prob = np.zeros(vocab)
+    prob[toks] = wts / wts.sum()
+    rows = 2048
+    spx = workloads.spx_module()
+    d_logits = torch.from_numpy(logits).cuda().expand(rows, vocab).contiguous()
+    d_params = spx.device_params(np.repeat(p, rows))
+    counts = np.zeros(vocab, dtype=np.int64)
+    draws = 400 * 64
+    done = 0
+    while done < draws:
+        n = min(rows, draws - done)
+        du = torch.from_numpy(np.array([rng.uniform() for _ in range(n)])).cuda()
+        ids, status = sampler.sample_rows(d_logits[:n], d_params[:n], du)
+        torch.cuda.synchronize()
+        assert (status.cpu().numpy() == 0).all()
+        counts += np.bincount(ids.cpu().numpy(), minlength=vocab)
+        done += n
+    share = counts / draws
+    assert not np.any((prob == 0) & (counts > 0)), "a token that is no candidate was picked"
+    dev = np.abs(share - prob) / (np.sqrt(prob * (1 - prob) / draws) + 1 / draws)
+    assert dev.max() <= 5.0, (int(np.argmax(dev)), dev.max())
+
+
+def test_long_histories(sampler):
+    # Histories of 8192 ids (the talker's grows one id per frame without a bound), with repetition, presence and
+    # frequency penalties, on both work-group sizes.
+    spx = workloads.spx_module()
+    big = spx.Sampler(max_rows=8, max_vocab=151936, max_hist=8192, max_out=MAX_OUT)
+    rng = np.random.default_rng(29)
+    for vocab in (151936, 3072):
+        rows = 4
+        logits = workloads.zipf_logits(rng, rows, vocab)
+        hists = [np.concatenate([np.argsort(-logits[r])[:100].repeat(8), rng.integers(0, vocab, 7392)]) for r in range(rows)]
+        hist, off = workloads.csr(hists)
+        p = spx.row_params(rows, temperature=0.8, top_k=np.array([0, 50, 0, 300]), top_p=0.9,
+                           repetition_penalty=1.1, presence_penalty=0.3,
+                           frequency_penalty=np.array([0.0, 0.05, 0.1, 0.0], dtype=np.float32))
+        w = workloads.Workload(name=f"hist 8192 x {vocab}", logits=logits, dtype="f32", params=p,
+                               u=workloads.uniforms(31, rows), hist=hist, hist_off=off, banned=None, banned_stride=0)
+        check(big, w)
