@@ -134,6 +134,12 @@ class Sampler:
             out_ids = torch.empty(rows, dtype=torch.int32, device=dev)
         if out_status is None:
             out_status = torch.empty(rows, dtype=torch.int32, device=dev)
+        for t, dt in ((out_ids, torch.int32), (out_status, torch.int32), (out_kept, torch.int32)):
+            if t is not None and (t.dtype != dt or t.numel() < rows or not t.is_contiguous()):
+                raise ValueError("per-row outputs are contiguous int32 tensors of at least rows entries")
+        for t, dt in ((out_cand_ids, torch.int32), (out_cand_weights, torch.float64)):
+            if t is not None and (t.dtype != dt or t.numel() < rows * self.max_out or not t.is_contiguous()):
+                raise ValueError("candidate outputs are contiguous tensors of rows x max_out (the handle's)")
         s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
         self._check(self.lib.spx_sample_rows(
             self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(hist), _ptr(hist_off), _ptr(banned),

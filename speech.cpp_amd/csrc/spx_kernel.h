@@ -990,8 +990,10 @@ __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx
     const bool full_known = nk >= pl.k || complete;
     const bool last_held = nk >= pl.k;  // the k-th candidate itself is held
     // Transformers and Haru normalize over their top k; beyond the entries held, only a top k of the whole
-    // vocabulary has a known sum (the stream's). Other rows take the multi-pass path.
+    // vocabulary has a known sum (the stream's). Other rows take the wide path. Haru's sum is a float32 sum in the
+    // row's order, which only the wide path takes beyond the entries held.
     if (!full_known && pl.k < a.vocab && pl.flavor != SPX_FLAVOR_FISH) return false;
+    if (!full_known && pl.flavor == SPX_FLAVOR_HARU) return false;
     // The sum of exp over the whole vocabulary, relative to the top value (m of the totals is that value or below).
     const double s_all = pl.need_s ? tot.s * exp((double) tot.m - (double) top) : 0.0;
     bool valid[4];
@@ -1278,39 +1280,75 @@ struct FbRow {
     uint32_t * n_own;
 };
 
-// Visits every token of the row, chunk by chunk, each chunk's special tokens rebuilt in LDS: f(entry, final logit,
-// quotient, banned, id), the entry 0 for a NaN quotient. A banned token is visited as -inf, once.
+// Visits every token of the row, chunk by chunk: f(entry, final logit, quotient, banned, id), the entry 0 for a NaN
+// quotient; a banned token is visited as -inf, once; a history token with its penalized logit, once. The chunk's
+// special tokens are those the kernel built in LDS when the launch has one chunk per row, else they are rebuilt per
+// chunk. Whole 16-byte vectors are read a step ahead of the step being visited (kE tokens per lane per step), so that
+// a pass runs at the rate of the loads rather than their latency.
 template <typename T, int B, typename F>
 __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
+    constexpr int V = Elt<T>::V, U = Elt<T>::U;
     const Launch & a = *r.a;
     const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
     const bool spec = r.pl.pen || r.banned_row;
     const uint32_t ninf = order_key(-INFINITY);
+    const int tid = threadIdx.x;
+    // one token: its special bit, then its quotient
+    auto visit = [&](int c0, int i, float x) __attribute__((always_inline)) {
+        if (spec) {
+            const int o = i - c0;
+            if ((r.sp.kill[o >> 5] >> (o & 31)) & 1u) {
+                // history tokens are visited below; a banned one (history or not) here
+                if (r.banned_row && ((r.banned_row[i >> 5] >> (i & 31)) & 1u))
+                    f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
+                return;
+            }
+        }
+        const float q = div_rn(x, r.pl.t, r.pl.rt);
+        f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
+    };
     for (int c0 = 0; c0 < a.vocab; c0 += a.chunk) {
         const int c1 = min(a.vocab, c0 + a.chunk);
-        if (spec) {
+        if (spec && a.splits > 1) {
             __syncthreads();  // the previous chunk's special tokens are read no more
             uint32_t bad = 0;
             int h0, h1;
             hist_range(a, r.row, r.pl, h0, h1, bad);
             build_specials<B>(r.sp, c0, c1, r.pl, r.banned_row, a.hist, h0, h1, -1, r.n_own);
+        } else if (spec) {
+            r.sp.n_own = min((int) *r.n_own, r.sp.own_cap);  // built by the kernel for the whole row
         }
-        for (int i = c0 + threadIdx.x; i < c1; i += B) {
-            if (spec) {
-                const int o = i - c0;
-                if ((r.sp.kill[o >> 5] >> (o & 31)) & 1u) {
-                    // history tokens are visited below; a banned one (history or not) here
-                    if (r.banned_row && ((r.banned_row[i >> 5] >> (i & 31)) & 1u))
-                        f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
-                    continue;
+        const int ng = a.vec_ok ? (c1 - c0) / V : 0;  // whole vectors
+        const U32x4 * vp = (const U32x4 *) (rowp + c0);
+        constexpr int per = U * B;
+        U32x4 cur[U], nxt[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int g = tid + u * B;
+            cur[u] = g < ng ? vp[g] : U32x4{0u, 0u, 0u, 0u};
+        }
+        for (int g0 = 0; g0 < ng; g0 += per) {
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int g = g0 + per + tid + u * B;
+                nxt[u] = g < ng ? vp[g] : U32x4{0u, 0u, 0u, 0u};
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int g = g0 + tid + u * B;
+                if (g < ng) {
+                    float x[V];
+                    unpack<T>(cur[u], x);
+#pragma unroll
+                    for (int j = 0; j < V; j++) visit(c0, c0 + g * V + j, x[j]);
                 }
             }
-            const float x = load_one<T>(rowp + i);
-            const float q = div_rn(x, r.pl.t, r.pl.rt);
-            f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
+#pragma unroll
+            for (int u = 0; u < U; u++) cur[u] = nxt[u];
         }
+        for (int i = c0 + ng * V + tid; i < c1; i += B) visit(c0, i, load_one<T>(rowp + i));
         if (r.pl.pen) {
-            for (int k = threadIdx.x; k < r.sp.n_own; k += B) {
+            for (int k = tid; k < r.sp.n_own; k += B) {
                 int cnt;
                 const int id = own_token(r.sp, r.pl, k, cnt);
                 if (id < 0) continue;
@@ -1320,7 +1358,7 @@ __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
             }
         }
     }
-    if (spec) __syncthreads();
+    if (spec && a.splits > 1) __syncthreads();
 }
 
 // The first entry in falling order whose running count (by_mass false) or running mass reaches `target` (strict:
@@ -1677,6 +1715,207 @@ __device__ __forceinline__ void question_bins(const WideQ & q, const uint32_t * 
     }
 }
 
+// Haru's float32 exponential of a token: std::exp of the float difference from the largest quotient, in float
+// (src/families/haru/sampler.cpp:47), correctly rounded.
+__device__ __forceinline__ float haru_exp(float q, float top) {
+    return q > -INFINITY ? (float) exp((double) (q - top)) : 0.0f;
+}
+
+// Half a unit in the last place of a positive float s: a term below it leaves s as it is when added.
+__device__ __forceinline__ float half_ulp(float s) {
+    if (!(s > 0.0f)) return 0.0f;
+    const int e = (int) ((__float_as_uint(s) >> 23) & 0xffu);
+    return e > 24 ? __uint_as_float((uint32_t) (e - 24) << 23) : 0x1p-149f * 0.5f;
+}
+
+// Gathers the tokens of the contiguous bins b0..b1 (at most CAP of them) and writes them to out[] in the row's order:
+// out[i] is the token of rank pre_cnt[b0] + i.
+template <typename T, int B, int NB, int CAP>
+__device__ __forceinline__ void gather_in_order(FbRow & r, WideMem<NB, CAP> & m, float top, int b0, int b1,
+                                                uint64_t * out) {
+    const int tid = threadIdx.x;
+    const uint32_t base = m.pre_cnt[b0];
+    for (int b = b0 + tid; b <= b1; b += B) m.seg[b] = m.pre_cnt[b] - base;
+    __syncthreads();
+    fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
+        if (!e) return;
+        const int b = (banned || !(qq > -INFINITY)) ? NB : wide_bin<NB>(qq, top);
+        if (b < b0 || b > b1) return;
+        m.ent[atomicAdd(&m.seg[b], 1u)] = e;
+    });
+    __syncthreads();
+    const int n = (int) (m.pre_cnt[b1 + 1] - base);
+    for (int i = tid; i < n; i += B) {
+        const uint64_t e = m.ent[i];
+        const float qq = entry_value(e);
+        const int b = !(qq > -INFINITY) ? NB : wide_bin<NB>(qq, top);
+        const int s0 = (int) (m.pre_cnt[b] - base), s1 = (int) (m.pre_cnt[b + 1] - base);
+        int rho = 0;
+        for (int j = s0; j < s1; j++) rho += m.ent[j] > e ? 1 : 0;
+        out[s0 + rho] = e;
+    }
+    __syncthreads();
+}
+
+// The last bin of a batch starting at bin b0 whose tokens fit CAP; -1 when bin b0 alone holds more.
+template <int NB, int CAP>
+__device__ __forceinline__ int batch_end(const WideMem<NB, CAP> & m, int b0) {
+    if (m.pre_cnt[b0 + 1] - m.pre_cnt[b0] > (uint32_t) CAP) return -1;
+    int b1 = b0;
+    while (b1 < NB && m.pre_cnt[b1 + 2] - m.pre_cnt[b0] <= (uint32_t) CAP) b1++;
+    return b1;
+}
+
+// Haru's sums in float32, as src/families/haru/sampler.cpp:44-59 adds them, token after token in the row's order: the
+// sum of the top k exponentials (sum_f), and, with 0 < top_p < 1, the running sum of the probabilities that zeroes every
+// token whose sum before it reaches top_p. Both are taken by one lane over batches of bins gathered in order; the sum
+// stops at the first term below half a unit of it (every later term is smaller and leaves it as it is), the zeroing
+// once the running sum has passed top_p by two units (every later token is zeroed). Where top_p applies this also
+// resolves the row: its pick and its listed candidates. Returns 0: the row is not resolved here (the pick is left to
+// the fixed-point questions), 1: resolved, -1: a bin holds more tokens than a batch takes.
+template <typename T, int B, int NB, int CAP>
+__device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan & pl, FbRow & r, WideMem<NB, CAP> & m,
+                                          float top, uint64_t lowest, float & sum_out) {
+    const int tid = threadIdx.x;
+    const uint64_t k = (uint64_t) pl.k;
+    uint64_t * ord = m.mass;  // the batch in the row's order
+    float * sh = (float *) m.red;
+    // the sum of the top k exponentials
+    float sumf = 0.0f;
+    {
+        int b0 = 0;
+        bool stop = false;
+        while (!stop && b0 <= NB && m.pre_cnt[b0] < k) {
+            const int b1 = batch_end(m, b0);
+            if (b1 < 0) return -1;
+            gather_in_order<T, B>(r, m, top, b0, b1, ord);
+            if (tid == 0) {
+                const uint32_t base = m.pre_cnt[b0];
+                const int n = (int) (m.pre_cnt[b1 + 1] - base);
+                float s = sumf;
+                bool st = false;
+                for (int i = 0; i < n && !st; i++) {
+                    if (base + (uint32_t) i >= k) {
+                        st = true;
+                        break;
+                    }
+                    const float e = haru_exp(entry_value(ord[i]), top);
+                    if (e < half_ulp(s)) st = true;
+                    else s += e;
+                }
+                sh[0] = s;
+                sh[1] = st ? 1.0f : 0.0f;
+            }
+            __syncthreads();
+            sumf = sh[0];
+            stop = sh[1] != 0.0f;
+            __syncthreads();
+            b0 = b1 + 1;
+        }
+    }
+    sum_out = sumf;
+    if (!(pl.top_p > 0.0f && pl.top_p < 1.0f)) return 0;
+
+    // The zeroing, the weights' double sum, the listed candidates; then the pick. One lane keeps the state in LDS.
+    const float tp = pl.top_p;
+    const float stop_at = __uint_as_float(__float_as_uint(tp) + 2u);
+    const double u = a.u[row];
+    const int nl = a.out_cand_ids ? (int) min((uint64_t) a.max_out, k) : 0;
+    double * dsh = (double *) &m.red[4];
+    uint64_t * ush = &m.red[8];
+    // state: cum (float), done zeroing; total (double); pick found, cumulative share (double)
+    if (tid == 0) {
+        sh[0] = 0.0f;
+        sh[1] = 0.0f;
+        dsh[0] = 0.0;
+        dsh[1] = 0.0;
+        ush[0] = 0;
+        ush[1] = 0;
+    }
+    __syncthreads();
+    for (int sweep = 0; sweep < 2; sweep++) {
+        // sweep 0: the zeroing and the total of the weights; sweep 1: pick() over them
+        int b0 = 0;
+        bool stop = false;
+        while (!stop && b0 <= NB && m.pre_cnt[b0] < k) {
+            const int b1 = batch_end(m, b0);
+            if (b1 < 0) return -1;
+            gather_in_order<T, B>(r, m, top, b0, b1, ord);
+            const uint32_t base = m.pre_cnt[b0];
+            const int n = (int) (m.pre_cnt[b1 + 1] - base);
+            if (tid == 0) {
+                float cum = sh[0];
+                bool st = false;
+                double total = dsh[0], share = dsh[1];
+                for (int i = 0; i < n && !st; i++) {
+                    const uint64_t rank = base + (uint64_t) i;
+                    if (rank >= k) {
+                        st = true;
+                        break;
+                    }
+                    const float e = haru_exp(entry_value(ord[i]), top);
+                    const float pr = e / sumf;
+                    const float c = cum + pr;
+                    const bool zero = !(c - pr < tp);
+                    cum = c;
+                    const double w = zero ? 0.0 : (double) pr;
+                    if (sweep == 0) {
+                        total += w;
+                        if (rank < (uint64_t) nl) {
+                            a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(ord[i]);
+                            a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = w;
+                        }
+                        if (zero && cum >= stop_at && rank + 1 >= (uint64_t) nl) st = true;
+                    } else {
+                        // src/common/sampling.cpp:9-19 over the k weights; its last is the k-th token
+                        share += w / total;
+                        if (rank + 1 < k && share > u) {
+                            ush[0] = 1;
+                            ush[1] = ord[i];
+                            st = true;
+                        } else if (zero && cum >= stop_at) {
+                            st = true;  // every later weight is 0: the share rises no more
+                        }
+                    }
+                }
+                sh[0] = cum;
+                sh[1] = st ? 1.0f : 0.0f;
+                dsh[0] = total;
+                dsh[1] = share;
+            }
+            __syncthreads();
+            stop = sh[1] != 0.0f;
+            __syncthreads();
+            b0 = b1 + 1;
+        }
+        if (tid == 0) {
+            sh[0] = 0.0f;
+            sh[1] = 0.0f;
+            dsh[1] = 0.0;
+        }
+        __syncthreads();
+    }
+    // no weight passed u before the last of the k: pick() answers the k-th token
+    uint64_t pick = ush[0] ? ush[1] : 0;
+    if (!pick && k == (uint64_t) a.vocab) {
+        pick = lowest;
+    } else if (!pick) {
+        const int b = bin_of_rank<NB>(m.pre_cnt, k - 1);
+        if (m.pre_cnt[b + 1] - m.pre_cnt[b] > (uint32_t) CAP) return -1;
+        gather_in_order<T, B>(r, m, top, b, b, ord);
+        pick = ord[k - 1 - m.pre_cnt[b]];
+    }
+    if (tid == 0) {
+        write_row(a, row, (int) entry_id(pick), SPX_ROW_OK, (int) k);
+        atomicAdd(a.fb_count, 1);
+    }
+    for (int j = nl + tid; j < a.max_out && a.out_cand_ids; j += B) {
+        a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
+        a.out_cand_w[(int64_t) row * a.max_out + j] = 0.0;
+    }
+    return 1;
+}
+
 // The row's answers from its histogram and at most a few gathering reads. Returns false when a question's bins hold
 // more tokens than LDS takes (the caller then takes the radix path).
 template <typename T, int B>
@@ -1763,6 +2002,14 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
     }
     const uint64_t total = m.pre_mass[NB + 1];
     const uint64_t lowest = m.lo_e;
+    // Haru's float32 sums, token after token: the zeroing rows are resolved there, the others keep its sum of the top k
+    // for their listed weights and draw by the questions below
+    float haru_sum = 1.0f;
+    if (pl.flavor == SPX_FLAVOR_HARU) {
+        const int h = haru_exact<T, B>(a, row, pl, r, m, top, lowest, haru_sum);
+        if (h < 0) return false;
+        if (h > 0) return true;
+    }
 
     // The questions of the row's flavor (the rules of src/families/qwen3-tts/sampler.cpp:77-99,
     // src/families/haru/sampler.cpp:36-59, src/families/drama3/sampler.cpp:44-59 and src/common/sampling.cpp:9-19).
@@ -1887,15 +2134,159 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
         }
     };
 
+    // A question whose target is known but whose one bin holds more tokens than a read gathers: a finer histogram of
+    // that bin alone (SNB sub-bins: the bin's quotient range cut evenly; the last finite bin's over the 64 below it;
+    // the -inf bin's by token id, its order), then a read that gathers the sub-bin holding the target.
+    constexpr int SNB = NB / 2;
+    auto refine = [&](int i) -> bool {
+        WideQ & Q = q[i];
+        int b, b1;
+        question_bins<NB>(Q, m.pre_cnt, m.pre_mass, b, b1);
+        if (b > NB) {  // no token reaches the target
+            Q.done = true;
+            Q.entry = 0;
+            Q.before = Q.through = total;
+            Q.rank = ~0u;
+            return true;
+        }
+        auto sub_of = [&](float qq, int id) {
+            if (b == NB) return (int) (((uint64_t) id * (uint64_t) SNB) / (uint64_t) a.vocab);
+            const float x = (top - qq) * kWideScale - (float) b;
+            const float y = b == NB - 1 ? x * ((float) SNB / 64.0f) : x * (float) SNB;
+            return y < (float) (SNB - 1) ? max((int) y, 0) : SNB - 1;
+        };
+        auto in_bin = [&](uint64_t e, float qq, bool banned) {
+            const bool ninf = banned || !(qq > -INFINITY);
+            return e != 0 && (ninf ? NB : wide_bin<NB>(qq, top)) == b;
+        };
+        uint32_t * scnt = (uint32_t *) m.ent;
+        uint64_t * smass = m.mass;
+        for (int j = tid; j <= SNB; j += B) {
+            scnt[j] = 0u;
+            smass[j] = 0ull;
+        }
+        __syncthreads();
+        fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
+            if (!in_bin(e, qq, banned)) return;
+            const int sb = sub_of(qq, id);
+            atomicAdd(&scnt[sb], 1u);
+            const uint64_t fm = (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
+            if (fm) atomicAdd((unsigned long long *) &smass[sb], (unsigned long long) fm);
+        });
+        __syncthreads();
+        // the sub-bin of the target, by one lane
+        if (tid == 0) {
+            uint32_t c = m.pre_cnt[b];
+            uint64_t ms = m.pre_mass[b];
+            int sb = -1;
+            for (int j = 0; j < SNB && sb < 0; j++) {
+                const uint32_t c1 = c + scnt[j];
+                const uint64_t m1 = ms + smass[j];
+                bool here;
+                if (Q.kind == kQRank) here = Q.lo < (uint64_t) c1;
+                else if (Q.kind == kQGe) here = Q.lo == 0 ? true : m1 >= Q.lo;
+                else here = m1 > Q.lo;
+                if (here && scnt[j] > 0) sb = j;
+                else {
+                    c = c1;
+                    ms = m1;
+                }
+            }
+            m.ans[0].found = sb >= 0 ? 1u : 0u;
+            m.ans[0].rank = (uint32_t) max(sb, 0);
+            m.ans[0].before = ms;
+            m.ans[0].through = c;
+            m.n_gath = sb >= 0 ? scnt[sb] : 0u;
+        }
+        __syncthreads();
+        const int sb = (int) m.ans[0].rank;
+        const bool found = m.ans[0].found != 0u;
+        const uint64_t base_m = m.ans[0].before, base_c = m.ans[0].through;
+        const int ng = (int) m.n_gath;
+        __syncthreads();
+        if (!found) {
+            Q.done = true;
+            Q.entry = 0;
+            Q.before = Q.through = total;
+            Q.rank = ~0u;
+            return true;
+        }
+        if (ng > CAP) return false;
+        if (tid == 0) m.n_gath = 0u;
+        __syncthreads();
+        fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
+            if (!in_bin(e, qq, banned) || sub_of(qq, id) != sb) return;
+            const uint32_t pos = atomicAdd(&m.n_gath, 1u);
+            m.ent[pos] = e;
+            m.mass[pos] = (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
+        });
+        for (int t = tid; t < kWideQs; t += B) m.ans[t].found = 0u;
+        __syncthreads();
+        for (int x = tid; x < ng; x += B) {
+            const uint64_t e = m.ent[x];
+            uint32_t rho = 0;
+            uint64_t mu = 0;
+            for (int j = 0; j < ng; j++) {
+                if (m.ent[j] > e) {
+                    rho++;
+                    mu += m.mass[j];
+                }
+            }
+            const uint64_t rank = base_c + rho, before = base_m + mu, through = before + m.mass[x];
+            bool hit;
+            if (Q.kind == kQRank) hit = rank == Q.lo;
+            else if (Q.kind == kQGe) hit = Q.lo == 0 ? rank == 0 : (before < Q.lo && Q.lo <= through);
+            else hit = before <= Q.lo && Q.lo < through;
+            if (hit) {
+                m.ans[0].entry = e;
+                m.ans[0].before = before;
+                m.ans[0].through = through;
+                m.ans[0].rank = (uint32_t) rank;
+                m.ans[0].found = 1u;
+            }
+        }
+        __syncthreads();
+        Q.done = true;
+        if (m.ans[0].found) {
+            Q.entry = m.ans[0].entry;
+            Q.before = m.ans[0].before;
+            Q.through = m.ans[0].through;
+            Q.rank = m.ans[0].rank;
+        } else {
+            Q.entry = 0;
+            Q.before = Q.through = total;
+            Q.rank = ~0u;
+        }
+        __syncthreads();
+        return true;
+    };
+
     // Gathering reads until every question is answered: each read takes the bins of the questions whose targets are
     // known, and while they fit those of the others' target ranges; the tokens it gathers then answer every question
     // whose target becomes known and whose bins they cover.
     constexpr int TPT = CAP / B;  // gathered tokens per thread
-    for (int round = 0; round < 6; round++) {
+    for (int round = 0; round < 12; round++) {
         targets();
         bool open = false;
         for (int i = 0; i < kWideQs; i++) open = open || (q[i].kind != kQNone && !q[i].done);
         if (!open) break;
+        // a known target whose bin alone is more than a read gathers: the finer histogram, then the next round
+        {
+            bool refined = false;
+            for (int i = 0; i < kWideQs && !refined; i++) {
+                if (q[i].kind == kQNone || q[i].done || !q[i].exact) continue;
+                int b0, b1;
+                question_bins<NB>(q[i], m.pre_cnt, m.pre_mass, b0, b1);
+                if (b0 > NB || m.pre_cnt[min(b1, NB) + 1] - m.pre_cnt[b0] <= (uint32_t) CAP) continue;
+                if (!refine(i)) return false;
+                refined = true;
+            }
+            if (refined) {
+                targets();
+                settle_pick();
+                continue;
+            }
+        }
         for (int i = tid; i < (NB + 1 + 31) / 32; i += B) m.need[i] = 0u;
         __syncthreads();
         uint32_t want = 0;
@@ -1907,10 +2298,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
                 uint32_t add = 0;
                 for (int b = b0; b <= b1 && b <= NB; b++)
                     if (!((m.need[b >> 5] >> (b & 31)) & 1u)) add += m.pre_cnt[b + 1] - m.pre_cnt[b];
-                if (want + add > (uint32_t) CAP) {
-                    if (pass == 0) return false;  // the bins of the known targets alone hold more than LDS takes
-                    continue;
-                }
+                if (want + add > (uint32_t) CAP) continue;  // gathered in a later round
                 want += add;
                 __syncthreads();
                 if (tid == 0)
@@ -2074,7 +2462,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
         const double w = ninf ? 0.0 : exp((double) qq - (double) top);
         double out;
         if (fl == SPX_FLAVOR_TRANSFORMERS) out = w / sk;
-        else if (fl == SPX_FLAVOR_HARU) out = rank < kept_n ? (double) (float) (w / sk) : 0.0;
+        else if (fl == SPX_FLAVOR_HARU) out = rank < kept_n ? (double) (haru_exp(qq, top) / haru_sum) : 0.0;
         else out = w;
         a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(e);
         a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = out;

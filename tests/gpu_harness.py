@@ -27,8 +27,9 @@ def to_device(w, device="cuda"):
 
 
 def run_gpu(sampler, w, d=None, max_out=0):
-    """The device's ids, statuses, kept counts and candidate outputs for a workload."""
+    """The device's ids, statuses, kept counts and candidate outputs for a workload (max_out: the handle's)."""
     import torch
+    assert not max_out or max_out == sampler.max_out, "candidate outputs are rows x the handle's max_out"
     d = d or to_device(w)
     rows = w.rows
     dev = d["logits"].device
@@ -59,7 +60,7 @@ def final_logits_row(w, r):
         words = w["banned"][0 if w["banned_stride"] == 0 else r]
         i = np.arange(w.vocab)
         b = ((words[i >> 5] >> (i & 31).astype(np.uint32)) & 1).astype(np.uint8)
-    return oracle_lib.final_logits(w.logits_f32()[r], w["params"][r], h, b)[1]
+    return oracle_lib.final_logits(w.row_f32(r), w["params"][r], h, b)[1]
 
 
 def compare(w, gpu, reports, cand_ids=None, cand_weights=None):

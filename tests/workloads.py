@@ -125,6 +125,10 @@ class Workload(dict):
     def logits_f32(self):
         return bf16_bits_to_f32(self["logits"]) if self["dtype"] == "bf16" else self["logits"]
 
+    def row_f32(self, r):
+        """Row r's logits as float32 (bfloat16 rows widened alone, not the whole batch)."""
+        return bf16_bits_to_f32(self["logits"][r]) if self["dtype"] == "bf16" else self["logits"][r]
+
 
 def make(name, rows=None, seed=1234):
     spx = spx_module()
