@@ -57,11 +57,38 @@ size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool ha
     off = align_up(off, 16);
     a.off_cand = (int) off;
     a.off_sort = (int) (off + (size_t) a.cand_cap * 8);
-    if (!greedy_only) {
-        const size_t wide = block == kBlockBig ? wide_lds_bytes<kBlockBig>() : wide_lds_bytes<kBlockSmall>();
-        off = std::max((size_t) a.off_sort + (size_t) kSortCap * 8, off + wide);
-    }
+    if (!greedy_only) off = (size_t) a.off_sort + (size_t) kSortCap * 8;
     a.lds_bytes = (int) off;
+    return off;
+}
+
+// The resolving kernel's launch record from the sampling one: a whole row per work-group (its special tokens over the
+// whole vocabulary), 1024 threads for large vocabularies, and an LDS layout whose last region is the wide path's (the
+// radix path's 2 x kKeep listed entries and its histograms fit there too).
+size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist) {
+    using namespace spx;
+    r = a;
+    r.block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
+    r.splits = 1;
+    r.chunk = a.vocab;
+    size_t off = 0;
+    r.off_ctl = (int) off;
+    off += kCtlBytes;
+    r.off_red = (int) off;
+    off += 1280;
+    r.off_spec = (int) off;
+    off += align_up((size_t) (a.vocab + 31) / 32 * 4, 16);
+    size_t cap = 1;
+    while (cap < (size_t) max_hist) cap *= 2;
+    r.own_cap = (int) cap;
+    r.off_own = (int) off;
+    off += cap * 4;
+    off = align_up(off, 16);
+    r.off_cand = (int) off;
+    r.off_sort = (int) (off + 2 * kKeep * 8);
+    const size_t wide = r.block == kBlockBig ? wide_lds_bytes<kBlockBig>() : wide_lds_bytes<kBlockSmall>();
+    off = std::max((size_t) r.off_sort + 3 * 1024, off + wide);
+    r.lds_bytes = (int) off;
     return off;
 }
 
@@ -109,6 +136,13 @@ hipError_t launch_sampler(const spx::Launch & a, hipStream_t s) {
     return a.dtype == SPX_BF16 ? launch_bf16_256(a, s) : launch_f32_256(a, s);
 }
 
+// The resolving kernel after a sampling launch: `grid` work-groups take the rows the sampling kernel left, if any.
+hipError_t launch_resolver(const spx::Launch & r, int grid, hipStream_t s) {
+    using namespace spx;
+    if (r.block == kBlockBig) return r.dtype == SPX_BF16 ? resolve_bf16_1024(r, grid, s) : resolve_f32_1024(r, grid, s);
+    return r.dtype == SPX_BF16 ? resolve_bf16_256(r, grid, s) : resolve_f32_256(r, grid, s);
+}
+
 // Lets every variant take `bytes` of dynamic LDS (above the 64 KiB a launch gets without asking).
 hipError_t set_lds_limits(int bytes) {
     using namespace spx;
@@ -153,6 +187,11 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
         Launch probe{};
         lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
     }
+    {
+        Launch probe{}, res{};
+        probe.vocab = max_vocab;
+        lds_max = std::max(lds_max, plan_resolve(res, probe, max_hist));
+    }
     if (lds_max > 160 * 1024) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
@@ -167,7 +206,8 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     const size_t n_partials = align_up((size_t) max_rows * kMaxSplitsGreedy * sizeof(Partial), 256);
     const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
     const size_t n_fb = 256;
-    const size_t bytes = n_counters + n_partials + n_cands + n_fb;
+    const size_t n_pending = align_up((size_t) max_rows * sizeof(Pending), 256);
+    const size_t bytes = n_counters + n_partials + n_cands + n_fb + n_pending;
     e = hipMalloc(&s->ws, bytes);
     if (e != hipSuccess) {
         delete s;
@@ -188,6 +228,9 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     s->base.part_cands = (uint64_t *) p;
     p += n_cands;
     s->base.fb_count = (int32_t *) p;
+    s->base.pend_ctr = (uint32_t *) (p + 64);
+    p += n_fb;
+    s->base.pending = (Pending *) p;
     s->base.max_hist = max_hist;
     *out = s;
     return SPX_OK;
@@ -235,6 +278,11 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
     hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
+    // the rows the sampling kernel left, resolved by a work-group each (a launch that finds none ends at once)
+    spx::Launch r;
+    plan_resolve(r, a, s->max_hist);
+    e = launch_resolver(r, std::min(rows, s->cus), (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "resolve_kernel launch");
     return SPX_OK;
 }
 

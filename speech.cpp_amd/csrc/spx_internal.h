@@ -75,6 +75,15 @@ struct Partial {
     int32_t pad;
 };
 
+// A row the one-pass kernel leaves to the resolving kernel: its status flags and its largest final quotient (NaN where
+// the one-pass kernel does not know it).
+struct Pending {
+    int32_t row;
+    uint32_t flags;
+    float top;
+    int32_t pad;
+};
+
 struct Launch {
     const void * logits;
     int64_t ld;
@@ -101,7 +110,9 @@ struct Launch {
     uint32_t * counters;   // [max_rows], each back to 0 after its row's last chunk
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]
     uint64_t * part_cands; // [max_rows * kMaxSplits * kKeep]
-    int32_t * fb_count;    // rows the multi-pass path has resolved since the handle was made
+    int32_t * fb_count;    // rows resolved past the one-pass path since the handle was made
+    Pending * pending;     // [max_rows]: the rows left to the resolving kernel
+    uint32_t * pend_ctr;   // [4]: rows left, rows taken, work-groups done (back to 0 after each resolving launch)
 };
 
 }  // namespace spx
@@ -109,11 +120,17 @@ struct Launch {
 #include <hip/hip_runtime.h>
 
 namespace spx {
-// The kernel's variants (spx_k_*.hip): logits of fp32 or bf16, work-groups of 1024 or 256 threads.
+// The kernels' variants (spx_k_*.hip): logits of fp32 or bf16, work-groups of 1024 or 256 threads. Each variant has
+// the one-pass sampling kernel (launch_*) and the kernel that resolves the rows it leaves (resolve_*); lds_limit_*
+// lets both take `bytes` of dynamic LDS.
 hipError_t launch_f32_1024(const Launch & a, hipStream_t s);
 hipError_t launch_bf16_1024(const Launch & a, hipStream_t s);
 hipError_t launch_f32_256(const Launch & a, hipStream_t s);
 hipError_t launch_bf16_256(const Launch & a, hipStream_t s);
+hipError_t resolve_f32_1024(const Launch & a, int grid, hipStream_t s);
+hipError_t resolve_bf16_1024(const Launch & a, int grid, hipStream_t s);
+hipError_t resolve_f32_256(const Launch & a, int grid, hipStream_t s);
+hipError_t resolve_bf16_256(const Launch & a, int grid, hipStream_t s);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);
 hipError_t lds_limit_f32_256(int bytes);

@@ -1245,6 +1245,11 @@ __device__ __forceinline__ int gather_sort(const uint64_t * buf, int nb, uint64_
     return total;
 }
 
+// The kernel's launch record where the kernel's arguments lie in memory (it is the kernel's one argument).
+__device__ __forceinline__ const Launch * kernel_args() {
+    return (const Launch *) __builtin_amdgcn_kernarg_segment_ptr();
+}
+
 // ------------------------------------------------------------------------------------------------------------------
 // The multi-pass path: exact radix selects over the whole row
 // ------------------------------------------------------------------------------------------------------------------
@@ -1438,7 +1443,7 @@ __device__ __forceinline__ void fallback_row(const Launch & a, int row, const sp
     uint32_t * hist_n = (uint32_t *) (lds + a.off_sort);
     unsigned long long * hist_m = (unsigned long long *) (lds + a.off_sort + 1024);
     FbRow r;
-    r.a = &a;
+    r.a = kernel_args();
     r.row = row;
     r.p = p;
     r.pl = pl;
@@ -1927,7 +1932,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
     const int tid = threadIdx.x;
     const int shift = 62 - (a.vocab > 1 ? 32 - __builtin_clz((uint32_t) (a.vocab - 1)) : 0);
     FbRow r;
-    r.a = &a;
+    r.a = kernel_args();
     r.row = row;
     r.p = p;
     r.pl = pl;
@@ -2473,12 +2478,15 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
 // A row the one-pass path could not finish: its status from the stream's flags and its largest quotient, then the
 // wide path, or where the bins it needs hold more tokens than LDS takes, the radix path. `top`: the largest final
 // quotient where the one-pass path knows it (its sorted candidates' first), else NaN, and a read finds it.
+// The launch record is read where the kernel's arguments lie (ka), so that the kernel keeps no copy of it in scratch
+// memory.
 template <typename T, int B>
-__device__ __forceinline__ void resolve_row(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
+__device__ __forceinline__ void resolve_row(const Launch * ka, int row, const spx_row_params & p, const Plan & pl,
                                             uint32_t F, float top, unsigned char * lds) {
+    const Launch & a = *ka;
     if (__builtin_isnan(top)) {
         FbRow r;
-        r.a = &a;
+        r.a = kernel_args();
         r.row = row;
         r.p = p;
         r.pl = pl;
@@ -2503,6 +2511,19 @@ __device__ __forceinline__ void resolve_row(const Launch & a, int row, const spx
     if (wide_row<T, B>(a, row, p, pl, top, lds)) return;
     __syncthreads();
     fallback_row<T, B>(a, row, p, pl, F, lds);
+}
+
+// Leaves a row to the resolving kernel, which runs after this kernel on the same stream.
+__device__ __forceinline__ void defer_row(const Launch & a, int row, uint32_t flags, float top) {
+    if (threadIdx.x == 0) {
+        const uint32_t i = atomicAdd(&a.pend_ctr[0], 1u);
+        Pending pe;
+        pe.row = row;
+        pe.flags = flags;
+        pe.top = top;
+        pe.pad = 0;
+        a.pending[i] = pe;
+    }
 }
 
 // ------------------------------------------------------------------------------------------------------------------
@@ -2696,8 +2717,7 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
         if (broken || !finish_block<B>(a, row, p, pl, t, cand, ntot, complete, pf, ctl)) {
             // the largest quotient: the sorted candidates' first, unless entries were dropped
             const float top = broken ? NAN : (ntot > 0 ? entry_value(cand[0]) : -INFINITY);
-            __syncthreads();
-            resolve_row<T, B>(a, row, p, pl, F, top, lds);
+            defer_row(a, row, F, top);
         }
         return;
     }
@@ -2753,8 +2773,7 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
     }
     if (any_broken || !finish_block<B>(a, row, p, pl, t, cand, tot, all_complete, pf, ctl)) {
         const float top = any_broken ? NAN : (tot > 0 ? entry_value(cand[0]) : -INFINITY);
-        __syncthreads();
-        resolve_row<T, B>(a, row, p, pl, t.flags, top, lds);
+        defer_row(a, row, t.flags, top);
     }
 }
 
@@ -2917,17 +2936,66 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
 }
 
+// The rows the one-pass kernel left: each work-group takes them one after another from the list, builds the row's
+// special tokens over the whole row, and resolves it by the wide path (or the radix path). The last work-group to
+// finish empties the list for the next call. The launch record is this kernel's own: one chunk per row, and the LDS
+// layout of the wide path.
+template <typename T, int B>
+__global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
+    extern __shared__ __align__(16) unsigned char lds[];
+    const int tid = threadIdx.x;
+    Ctl * ctl = (Ctl *) (lds + a.off_ctl);
+    const uint32_t n = a.pend_ctr[0];
+    for (;;) {
+        if (tid == 0) ctl->last = atomicAdd(&a.pend_ctr[1], 1u);
+        __syncthreads();
+        const uint32_t idx = ctl->last;
+        __syncthreads();
+        if (idx >= n) break;
+        const Pending pe = a.pending[idx];
+        const int row = pe.row;
+        const spx_row_params p = a.params[row];
+        const Plan pl = make_plan(p, a.vocab, a.banned != nullptr, a.hist != nullptr, a.max_out);
+        const uint32_t * banned_row = a.banned ? a.banned + (int64_t) row * a.banned_stride : nullptr;
+        uint32_t bad = 0;
+        int h0, h1;
+        hist_range(a, row, pl, h0, h1, bad);
+        Specials sp;
+        specials_at(sp, a, lds);
+        if (pl.pen || banned_row) build_specials<B>(sp, 0, a.vocab, pl, banned_row, a.hist, h0, h1, -1, &ctl->n_own);
+        __syncthreads();
+        resolve_row<T, B>(kernel_args(), row, p, pl, pe.flags, pe.top, lds);
+        __syncthreads();
+    }
+    if (tid == 0) {
+        const uint32_t done = atomicAdd(&a.pend_ctr[2], 1u);
+        if (done == gridDim.x - 1) {
+            a.pend_ctr[0] = 0u;
+            a.pend_ctr[1] = 0u;
+            a.pend_ctr[2] = 0u;
+        }
+    }
+}
+
 }  // namespace spx
 
-// One variant of the kernel: its launcher and its LDS limit, named spx::launch_<NAME> and spx::lds_limit_<NAME>.
+// One variant of the kernels: the launchers spx::launch_<NAME> and spx::resolve_<NAME>, and their LDS limit
+// spx::lds_limit_<NAME>.
 #define SPX_KERNEL_VARIANT(T, B, NAME)                                                                          \
     namespace spx {                                                                                             \
     hipError_t launch_##NAME(const Launch & a, hipStream_t s) {                                                 \
         hipLaunchKernelGGL((sampler_kernel<T, B>), dim3(a.nwg), dim3(B), a.lds_bytes, s, a);                    \
         return hipGetLastError();                                                                               \
     }                                                                                                           \
+    hipError_t resolve_##NAME(const Launch & a, int grid, hipStream_t s) {                                       \
+        hipLaunchKernelGGL((resolve_kernel<T, B>), dim3(grid), dim3(B), a.lds_bytes, s, a);                     \
+        return hipGetLastError();                                                                               \
+    }                                                                                                           \
     hipError_t lds_limit_##NAME(int bytes) {                                                                    \
-        return hipFuncSetAttribute((const void *) sampler_kernel<T, B>, hipFuncAttributeMaxDynamicSharedMemorySize, \
+        hipError_t e = hipFuncSetAttribute((const void *) sampler_kernel<T, B>,                                 \
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                  \
+        if (e != hipSuccess) return e;                                                                          \
+        return hipFuncSetAttribute((const void *) resolve_kernel<T, B>, hipFuncAttributeMaxDynamicSharedMemorySize, \
                                    bytes);                                                                      \
     }                                                                                                           \
     }
