@@ -18,6 +18,7 @@ struct spx_sampler {
     void * ws = nullptr;
     spx::Launch base{};
     int last_block = 0, last_splits = 0;
+    int parity = 0;  // the slot of the resolving list's count this call uses
 };
 
 namespace {
@@ -68,7 +69,7 @@ size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool ha
 size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist) {
     using namespace spx;
     r = a;
-    r.block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
+    r.block = a.vocab >= kBigVocab ? kBlockResolve : kBlockSmall;
     r.splits = 1;
     r.chunk = a.vocab;
     size_t off = 0;
@@ -86,7 +87,7 @@ size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist) {
     off = align_up(off, 16);
     r.off_cand = (int) off;
     r.off_sort = (int) (off + 2 * kKeep * 8);
-    const size_t wide = r.block == kBlockBig ? wide_lds_bytes<kBlockBig>() : wide_lds_bytes<kBlockSmall>();
+    const size_t wide = r.block == kBlockResolve ? wide_lds_bytes<kBlockResolve>() : wide_lds_bytes<kBlockSmall>();
     off = std::max((size_t) r.off_sort + 3 * 1024, off + wide);
     r.lds_bytes = (int) off;
     return off;
@@ -139,7 +140,7 @@ hipError_t launch_sampler(const spx::Launch & a, hipStream_t s) {
 // The resolving kernel after a sampling launch: `grid` work-groups take the rows the sampling kernel left, if any.
 hipError_t launch_resolver(const spx::Launch & r, int grid, hipStream_t s) {
     using namespace spx;
-    if (r.block == kBlockBig) return r.dtype == SPX_BF16 ? resolve_bf16_1024(r, grid, s) : resolve_f32_1024(r, grid, s);
+    if (r.block == kBlockResolve) return r.dtype == SPX_BF16 ? resolve_bf16_1024(r, grid, s) : resolve_f32_1024(r, grid, s);
     return r.dtype == SPX_BF16 ? resolve_bf16_256(r, grid, s) : resolve_f32_256(r, grid, s);
 }
 
@@ -276,6 +277,8 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_cand_w = d_out_cand_weights;
     a.max_out = d_out_cand_ids ? s->max_out : 0;
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
+    a.parity = s->parity;
+    s->parity ^= 1;
     hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     // the rows the sampling kernel left, resolved by a work-group each (a launch that finds none ends at once)

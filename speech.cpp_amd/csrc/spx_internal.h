@@ -12,6 +12,8 @@ namespace spx {
 // 256 below.
 constexpr int kBlockBig = 1024;
 constexpr int kBlockSmall = 256;
+// Threads per work-group of the resolving kernel for large vocabularies (256 below): up to 256 VGPRs per lane.
+constexpr int kBlockResolve = 512;
 constexpr int kBigVocab = 16384;
 // Final logits each lane holds per step of the stream (four 16-byte vectors of fp32, two of bf16).
 constexpr int kE = 16;
@@ -31,6 +33,11 @@ template <int B>
 struct WideDims;
 template <>
 struct WideDims<1024> {
+    static constexpr int NB = 2048;
+    static constexpr int CAP = 2048;
+};
+template <>
+struct WideDims<512> {
     static constexpr int NB = 2048;
     static constexpr int CAP = 2048;
 };
@@ -112,7 +119,8 @@ struct Launch {
     uint64_t * part_cands; // [max_rows * kMaxSplits * kKeep]
     int32_t * fb_count;    // rows resolved past the one-pass path since the handle was made
     Pending * pending;     // [max_rows]: the rows left to the resolving kernel
-    uint32_t * pend_ctr;   // [4]: rows left, rows taken, work-groups done (back to 0 after each resolving launch)
+    uint32_t * pend_ctr;   // [4]: the count of rows left and of rows taken, one of each per call parity
+    int parity;            // this call's slot of pend_ctr: calls alternate, so that no kernel has to clear its own
 };
 
 }  // namespace spx

@@ -2164,17 +2164,26 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             const bool ninf = banned || !(qq > -INFINITY);
             return e != 0 && (ninf ? NB : wide_bin<NB>(qq, top)) == b;
         };
+        // per sub-bin: count, mass, and the smallest and largest key (a sub-bin of one key is a run of equal tokens)
         uint32_t * scnt = (uint32_t *) m.ent;
+        uint32_t * smin = scnt + (SNB + 1);
+        uint32_t * smax = smin + SNB;
         uint64_t * smass = m.mass;
         for (int j = tid; j <= SNB; j += B) {
             scnt[j] = 0u;
             smass[j] = 0ull;
+            if (j < SNB) {
+                smin[j] = ~0u;
+                smax[j] = 0u;
+            }
         }
         __syncthreads();
         fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
             if (!in_bin(e, qq, banned)) return;
             const int sb = sub_of(qq, id);
             atomicAdd(&scnt[sb], 1u);
+            atomicMin(&smin[sb], entry_key(e));
+            atomicMax(&smax[sb], entry_key(e));
             const uint64_t fm = (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
             if (fm) atomicAdd((unsigned long long *) &smass[sb], (unsigned long long) fm);
         });
@@ -2202,18 +2211,80 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             m.ans[0].before = ms;
             m.ans[0].through = c;
             m.n_gath = sb >= 0 ? scnt[sb] : 0u;
+            m.ans[0].entry = sb >= 0 && smin[sb] == smax[sb] ? (uint64_t) smin[sb] + 1 : 0ull;  // its one key + 1
         }
         __syncthreads();
         const int sb = (int) m.ans[0].rank;
         const bool found = m.ans[0].found != 0u;
         const uint64_t base_m = m.ans[0].before, base_c = m.ans[0].through;
         const int ng = (int) m.n_gath;
+        const uint64_t one_key = m.ans[0].entry;
         __syncthreads();
         if (!found) {
             Q.done = true;
             Q.entry = 0;
             Q.before = Q.through = total;
             Q.rank = ~0u;
+            return true;
+        }
+        if (ng > CAP && one_key) {
+            // A run of ng equal tokens (bfloat16 logits make long ones): each weighs the same, so the target's place
+            // in the run is arithmetic, and the run's order is the tokens' order by id; the token at that place is
+            // found by a count over id ranges and a read that gathers one range.
+            const uint32_t key = (uint32_t) (one_key - 1);
+            const float qk = key_float(key);
+            const uint64_t m1 = qk > -INFINITY ? fixed_mass(qk, top, shift) : 0ull;
+            uint64_t j;
+            if (Q.kind == kQRank) j = Q.lo - base_c;
+            else if (m1 == 0) j = 0;
+            else if (Q.kind == kQGe) j = Q.lo == 0 ? 0 : (Q.lo - base_m + m1 - 1) / m1 - 1;
+            else j = (Q.lo - base_m) / m1;
+            if (j >= (uint64_t) ng) return false;
+            auto idbin = [&](int id) { return (int) (((uint64_t) id * (uint64_t) SNB) / (uint64_t) a.vocab); };
+            for (int x = tid; x <= SNB; x += B) scnt[x] = 0u;
+            __syncthreads();
+            fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
+                if (in_bin(e, qq, banned) && entry_key(e) == key) atomicAdd(&scnt[idbin(id)], 1u);
+            });
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t c = 0;
+                int ib = 0;
+                while (ib < SNB - 1 && (uint64_t) (c + scnt[ib]) <= j) c += scnt[ib++];
+                m.ans[0].rank = (uint32_t) ib;
+                m.ans[0].through = c;
+                m.n_gath = 0u;
+            }
+            __syncthreads();
+            const int ib = (int) m.ans[0].rank;
+            const uint64_t jb = j - m.ans[0].through;  // the place within the id range
+            const uint32_t nib = scnt[ib];
+            __syncthreads();
+            if (nib > (uint32_t) CAP) return false;
+            for (int t = tid; t < kWideQs; t += B) m.ans[t].found = 0u;
+            fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
+                if (!in_bin(e, qq, banned) || entry_key(e) != key || idbin(id) != ib) return;
+                m.ent[atomicAdd(&m.n_gath, 1u)] = e;
+            });
+            __syncthreads();
+            const int n2 = (int) m.n_gath;
+            for (int x = tid; x < n2; x += B) {
+                const uint64_t e = m.ent[x];
+                uint32_t rho = 0;
+                for (int y = 0; y < n2; y++) rho += m.ent[y] > e ? 1u : 0u;
+                if ((uint64_t) rho == jb) {
+                    m.ans[0].entry = e;
+                    m.ans[0].found = 1u;
+                }
+            }
+            __syncthreads();
+            if (!m.ans[0].found) return false;
+            Q.done = true;
+            Q.entry = m.ans[0].entry;
+            Q.rank = (uint32_t) (base_c + j);
+            Q.before = base_m + j * m1;
+            Q.through = Q.before + m1;
+            __syncthreads();
             return true;
         }
         if (ng > CAP) return false;
@@ -2516,7 +2587,7 @@ __device__ __forceinline__ void resolve_row(const Launch * ka, int row, const sp
 // Leaves a row to the resolving kernel, which runs after this kernel on the same stream.
 __device__ __forceinline__ void defer_row(const Launch & a, int row, uint32_t flags, float top) {
     if (threadIdx.x == 0) {
-        const uint32_t i = atomicAdd(&a.pend_ctr[0], 1u);
+        const uint32_t i = atomicAdd(&a.pend_ctr[a.parity], 1u);
         Pending pe;
         pe.row = row;
         pe.flags = flags;
@@ -2936,18 +3007,25 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     else greedy_row<T, B>(a, row, split, p, pl, c0, c1, rowp, banned_row, sp, bad, lds, first);
 }
 
-// The rows the one-pass kernel left: each work-group takes them one after another from the list, builds the row's
-// special tokens over the whole row, and resolves it by the wide path (or the radix path). The last work-group to
-// finish empties the list for the next call. The launch record is this kernel's own: one chunk per row, and the LDS
-// layout of the wide path.
+// The rows the one-pass kernel left: the work-groups take list entries one at a time, each row resolved with its
+// special tokens built over the whole row, by the wide path (or the radix path). A launch that finds the list empty
+// ends at once. The list's count and the count of entries taken are one of two slots that calls alternate between:
+// this kernel clears the other slots, which the next call uses, so that no kernel clears a count it reads. The launch record is this kernel's
+// own: one chunk per row, and the LDS layout of the wide path.
 template <typename T, int B>
 __global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
     extern __shared__ __align__(16) unsigned char lds[];
     const int tid = threadIdx.x;
+    if (blockIdx.x == 0 && tid == 0) {
+        a.pend_ctr[a.parity ^ 1] = 0u;
+        a.pend_ctr[2 + (a.parity ^ 1)] = 0u;
+    }
+    const uint32_t n = a.pend_ctr[a.parity];
+    if (n == 0) return;
     Ctl * ctl = (Ctl *) (lds + a.off_ctl);
-    const uint32_t n = a.pend_ctr[0];
     for (;;) {
-        if (tid == 0) ctl->last = atomicAdd(&a.pend_ctr[1], 1u);
+        // rows are taken one at a time, so that work-groups whose rows resolve fast take more of them
+        if (tid == 0) ctl->last = atomicAdd(&a.pend_ctr[2 + a.parity], 1u);
         __syncthreads();
         const uint32_t idx = ctl->last;
         __syncthreads();
@@ -2967,14 +3045,6 @@ __global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
         resolve_row<T, B>(kernel_args(), row, p, pl, pe.flags, pe.top, lds);
         __syncthreads();
     }
-    if (tid == 0) {
-        const uint32_t done = atomicAdd(&a.pend_ctr[2], 1u);
-        if (done == gridDim.x - 1) {
-            a.pend_ctr[0] = 0u;
-            a.pend_ctr[1] = 0u;
-            a.pend_ctr[2] = 0u;
-        }
-    }
 }
 
 }  // namespace spx
@@ -2988,14 +3058,15 @@ __global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
         return hipGetLastError();                                                                               \
     }                                                                                                           \
     hipError_t resolve_##NAME(const Launch & a, int grid, hipStream_t s) {                                       \
-        hipLaunchKernelGGL((resolve_kernel<T, B>), dim3(grid), dim3(B), a.lds_bytes, s, a);                     \
+        constexpr int RB = B == kBlockBig ? kBlockResolve : B;                                                  \
+        hipLaunchKernelGGL((resolve_kernel<T, RB>), dim3(grid), dim3(RB), a.lds_bytes, s, a);                   \
         return hipGetLastError();                                                                               \
     }                                                                                                           \
     hipError_t lds_limit_##NAME(int bytes) {                                                                    \
         hipError_t e = hipFuncSetAttribute((const void *) sampler_kernel<T, B>,                                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                  \
         if (e != hipSuccess) return e;                                                                          \
-        return hipFuncSetAttribute((const void *) resolve_kernel<T, B>, hipFuncAttributeMaxDynamicSharedMemorySize, \
-                                   bytes);                                                                      \
+        return hipFuncSetAttribute((const void *) resolve_kernel<T, B == kBlockBig ? kBlockResolve : B>,        \
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                          \
     }                                                                                                           \
     }

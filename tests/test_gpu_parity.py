@@ -213,6 +213,21 @@ def test_heavy_ban_leaves_few_tokens_across_the_vocabulary(sampler):
     check(sampler, w)
 
 
+def test_bf16_runs_of_equal_logits(sampler):
+    # bfloat16 logits of a narrow spread take few distinct values, in runs of thousands of equal tokens: the top-p cut
+    # and the pick land inside such runs, whose order is by id (the lower id first) for Haru and Drama 3.
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(33)
+    rows, vocab = 6, 151936
+    logits = workloads.to_bf16_bits(rng.normal(0, 0.5, (rows, vocab)).astype(np.float32))
+    flavor = np.array([0, 1, 2, 0, 1, 2])
+    p = spx.row_params(rows, flavor=flavor, temperature=1.0, top_k=np.array([0, 0, 100000, 70000, 0, 5000]),
+                       top_p=np.array([0.95, 0.5, 0.9, 1.0, 1.0, 0.8], dtype=np.float32))
+    w = workloads.Workload(name="bf16 runs", logits=logits, dtype="bf16", params=p, u=workloads.uniforms(35, rows),
+                           hist=None, hist_off=None, banned=None, banned_stride=0)
+    check(sampler, w)
+
+
 def test_repeated_calls_reuse_workspace(sampler):
     # The per-row counters and the fallback list reset themselves: calls in a row give the same answers.
     w = workloads.make("mixed", rows=64, seed=21)
