@@ -134,6 +134,50 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
 spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
                            const uint32_t * d_banned, int64_t banned_stride, int32_t * d_out_ids, void * stream);
 
+/*
+ * One pick of Qwen3-TTS's code-predictor chain for `rows` streams at once, kept on the device between the predictor's
+ * forwards: pick `step` (0-based: the frame's code step + 1) of every stream, drawn from d_logits (rows x vocab, the
+ * step's head) with the stream's codes picked so far this frame as the history, and written into the codes array
+ * where the next pick reads it. The penalties of d_params apply, repetition included, so that the picks stay on the
+ * device where GraphSampler (src/families/qwen3-tts/graph-sampler.h:18-57) falls back to the host for a repetition
+ * penalty other than 1 (src/families/qwen3-tts/talker.cpp:145-153). Replaces, per stream,
+ *   sample(logits, cp_sampling, cp_history, none, cp_draws[code - 1])   src/families/qwen3-tts/synthesizer.cpp:92-93,
+ *   with cp_history the frame's codes 1 .. code - 1                       :130-139
+ *   d_codes        rows x codes_stride int32 (codes_stride >= picks + 1): stream r's frame at d_codes + r*codes_stride,
+ *                  [0] the talker's first code, [1 .. step] the codes picked so far; pick `step` writes [step + 1]
+ *   d_params       rows spx_row_params (the code predictor's settings, per stream)
+ *   d_u            rows x picks doubles: stream r's uniform() numbers for its picks in order (r*picks + step is read;
+ *                  unread for greedy rows)
+ *   d_out_status   optional: rows int32 spx_row_status of this pick
+ * The handle's max_hist must be at least picks.
+ */
+spx_status spx_sample_chain(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                            int32_t * d_codes, int codes_stride, int step, int picks, const spx_row_params * d_params,
+                            const double * d_u, int32_t * d_out_status, void * stream);
+
+/*
+ * Drama 3's main token (FrameSampler::main, src/families/drama3/sampler.cpp:70-79) for `rows` rows at once: each row
+ * drawn twice from its logits, with the request's settings d_first and u d_u_first, and with the file's redraw settings
+ * d_again and u d_u_again (both SPX_FLAVOR_FISH); the first draw's id mapped through d_token_ids (the file's
+ * output.token_ids, one per logit) stands, unless it is a semantic id (semantic_begin .. semantic_end) among the last
+ * `window` ids of the row's history (CSR, d_hist / d_hist_off: the main tokens so far, may be null), where the redraw's
+ * mapped id stands. An error of either draw is the row's status, the first draw's first, as both candidates() calls
+ * run. The handle's max_rows must be at least 2 * rows.
+ */
+spx_status spx_drama3_main(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const spx_row_params * d_first, const spx_row_params * d_again, const double * d_u_first,
+                           const double * d_u_again, const int32_t * d_token_ids, int32_t semantic_begin,
+                           int32_t semantic_end, int window, const int32_t * d_hist, const int32_t * d_hist_off,
+                           int32_t * d_out_ids, int32_t * d_out_status, void * stream);
+
+/*
+ * The Qwen3-TTS talker's suppress mask as mask words (the layout of d_banned): Generation::banned(vocab,
+ * end_of_speech, frames) of src/families/qwen3-tts/sampler.cpp:62-67, the last suppressed_tokens ids banned except
+ * end_of_speech, and end_of_speech banned while frames < min_frames. Writes (vocab + 31) / 32 words on the stream.
+ */
+spx_status spx_talker_bans(uint32_t * d_words, int vocab, int suppressed_tokens, int32_t end_of_speech, int frames,
+                           int min_frames, void * stream);
+
 /* Message of the last failed call on this thread ("" when none). */
 const char * spx_last_error(void);
 

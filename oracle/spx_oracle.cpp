@@ -435,6 +435,37 @@ void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_
     for (auto & th : pool) th.join();
 }
 
+void orc_talker_bans(int vocab, int suppressed_tokens, int32_t end_of_speech, int frames, int min_frames,
+                     uint8_t * out) {
+    // Generation::banned: src/families/qwen3-tts/sampler.cpp:62-67
+    std::vector<bool> b((size_t) vocab, false);
+    for (int i = vocab - suppressed_tokens; i < vocab; i++) b[(size_t) i] = i != end_of_speech;
+    if (frames < min_frames) b[(size_t) end_of_speech] = true;
+    for (int i = 0; i < vocab; i++) out[i] = b[(size_t) i] ? 1 : 0;
+}
+
+int orc_drama3_main(const float * logits, int vocab, const spx_row_params * first, const spx_row_params * again,
+                    double u_first, double u_again, const int32_t * token_ids, int32_t semantic_begin,
+                    int32_t semantic_end, int window, const int32_t * history, int n_history, int32_t * out_id) {
+    // FrameSampler::main: src/families/drama3/sampler.cpp:70-79, both candidates() first
+    *out_id = -1;
+    std::vector<float> l(logits, logits + vocab);
+    for (float v : l) {
+        if (!std::isfinite(v)) return SPX_ROW_NONFINITE_INPUT;  // drama3/sampler.cpp:35-37, in either call
+    }
+    const Drawn drawn = fish_draw(l, first->temperature, first->top_k, first->top_p);
+    if (drawn.status != SPX_ROW_OK) return drawn.status;
+    const Drawn redrawn = fish_draw(l, again->temperature, again->top_k, again->top_p);
+    if (redrawn.status != SPX_ROW_OK) return redrawn.status;
+    const int32_t id = token_ids[drawn.tokens[(size_t) pick_index(drawn.weights, u_first)]];
+    const int32_t other = token_ids[redrawn.tokens[(size_t) pick_index(redrawn.weights, u_again)]];
+    const int from = n_history - std::min(window, n_history);
+    const bool recent = std::find(history + from, history + n_history, id) != history + n_history;
+    const bool semantic = id >= semantic_begin && id <= semantic_end;
+    *out_id = semantic && recent ? other : id;
+    return SPX_ROW_OK;
+}
+
 int orc_final_logits(const float * logits, int vocab, const spx_row_params * p, const int32_t * hist, int n_hist,
                      const uint8_t * banned, float * out) {
     std::vector<float> l(logits, logits + vocab);

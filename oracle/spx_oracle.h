@@ -79,6 +79,19 @@ void orc_sample_rows(const void * logits, int dtype, int rows, int vocab, int64_
 int orc_final_logits(const float * logits, int vocab, const spx_row_params * p, const int32_t * hist, int n_hist,
                      const uint8_t * banned, float * out);
 
+/* Generation::banned (src/families/qwen3-tts/sampler.cpp:62-67): out[i] = 1 for each banned id of the talker's frame. */
+void orc_talker_bans(int vocab, int suppressed_tokens, int32_t end_of_speech, int frames, int min_frames,
+                     uint8_t * out);
+
+/*
+ * FrameSampler::main (src/families/drama3/sampler.cpp:70-79) with the request's and the redraw's settings as two
+ * records (their temperature, top_k and top_p): the mapped id of the first draw, or of the redraw where the first is a
+ * semantic id among the last `window` ids of the history. Returns a spx_row_status.
+ */
+int orc_drama3_main(const float * logits, int vocab, const spx_row_params * first, const spx_row_params * again,
+                    double u_first, double u_again, const int32_t * token_ids, int32_t semantic_begin,
+                    int32_t semantic_end, int window, const int32_t * history, int n_history, int32_t * out_id);
+
 #ifdef __cplusplus
 }
 #endif

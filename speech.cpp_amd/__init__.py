@@ -30,8 +30,8 @@ ROW_PARAMS = np.dtype([("flavor", "<i4"), ("greedy", "<i4"), ("temperature", "<f
 assert ROW_PARAMS.itemsize == 32
 
 # Every symbol include/spx_sampler.h declares.
-EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_last_error",
-           "spx_sampler_last_stats"]
+EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_sample_chain",
+           "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats"]
 
 
 class SpxStats(ctypes.Structure):
@@ -62,6 +62,12 @@ def load_library(path=LIB_PATH):
     lib.spx_sample_rows.restype = i32
     lib.spx_argmax_rows.argtypes = [p, vp, i32, i32, i32, i64, vp, i64, vp, vp]
     lib.spx_argmax_rows.restype = i32
+    lib.spx_sample_chain.argtypes = [p, vp, i32, i32, i32, i64, vp, i32, i32, i32, vp, vp, vp, vp]
+    lib.spx_sample_chain.restype = i32
+    lib.spx_drama3_main.argtypes = [p, vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp]
+    lib.spx_drama3_main.restype = i32
+    lib.spx_talker_bans.argtypes = [vp, i32, i32, i32, i32, i32, vp]
+    lib.spx_talker_bans.restype = i32
     lib.spx_last_error.argtypes = []
     lib.spx_last_error.restype = ctypes.c_char_p
     lib.spx_sampler_last_stats.argtypes = [p, ctypes.POINTER(SpxStats)]
@@ -161,10 +167,57 @@ class Sampler:
                                              _ptr(banned), banned_stride, _ptr(out_ids), ctypes.c_void_p(s)))
         return out_ids
 
+    def sample_chain(self, logits, codes, step, params, u, out_status=None, stream=None):
+        """Pick `step` of the code-predictor chain: logits (streams x vocab), codes (streams x >= picks + 1 int32, row
+        r: [first code, picked codes...]), u (streams x picks float64). Writes codes[:, step + 1]."""
+        import torch
+        rows, vocab = logits.shape
+        picks = u.shape[1]
+        if codes.dtype != torch.int32 or not codes.is_contiguous() or codes.shape[0] < rows:
+            raise ValueError("codes are a contiguous int32 tensor of streams x (picks + 1) or more")
+        if u.dtype != torch.float64 or not u.is_contiguous():
+            raise ValueError("u is a contiguous float64 tensor of streams x picks")
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ld = logits.stride(0) if rows > 1 else vocab
+        s = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        self._check(self.lib.spx_sample_chain(self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(codes),
+                                              codes.shape[1], step, picks, _ptr(params), _ptr(u), _ptr(out_status),
+                                              ctypes.c_void_p(s)))
+
+    def drama3_main(self, logits, first, again, u_first, u_again, token_ids, semantic_begin, semantic_end, window,
+                    hist=None, hist_off=None, out_ids=None, out_status=None, stream=None):
+        import torch
+        rows, vocab = logits.shape
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ld = logits.stride(0) if rows > 1 else vocab
+        if out_ids is None:
+            out_ids = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        if out_status is None:
+            out_status = torch.empty(rows, dtype=torch.int32, device=logits.device)
+        s = stream if stream is not None else torch.cuda.current_stream(logits.device).cuda_stream
+        self._check(self.lib.spx_drama3_main(self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(first),
+                                             _ptr(again), _ptr(u_first), _ptr(u_again), _ptr(token_ids),
+                                             semantic_begin, semantic_end, window, _ptr(hist), _ptr(hist_off),
+                                             _ptr(out_ids), _ptr(out_status), ctypes.c_void_p(s)))
+        return out_ids, out_status
+
     def last_stats(self):
         st = SpxStats()
         self._check(self.lib.spx_sampler_last_stats(self.handle, ctypes.byref(st)))
         return st
+
+
+def talker_bans(vocab, suppressed_tokens, end_of_speech, frames, min_frames, device="cuda", stream=None):
+    """The talker's suppress mask (Generation::banned) built on the device, as int32 words."""
+    import torch
+    lib = load_library()
+    words = torch.empty((vocab + 31) // 32, dtype=torch.int32, device=device)
+    s = stream if stream is not None else torch.cuda.current_stream(words.device).cuda_stream
+    st = lib.spx_talker_bans(_ptr(words), vocab, suppressed_tokens, end_of_speech, frames, min_frames,
+                             ctypes.c_void_p(s))
+    if st != 0:
+        raise SamplerError(f"spx status {st}: {lib.spx_last_error().decode()}")
+    return words
 
 
 def device_params(params, device="cuda"):

@@ -19,6 +19,12 @@ struct spx_sampler {
     spx::Launch base{};
     int last_block = 0, last_splits = 0;
     int parity = 0;  // the slot of the resolving list's count this call uses
+    // the two-draw entry's records: max_rows each (a call draws 2 rows per row)
+    spx_row_params * pair_params = nullptr;
+    double * pair_u = nullptr;
+    int32_t * pair_map = nullptr;
+    int32_t * pair_ids = nullptr;
+    int32_t * pair_status = nullptr;
 };
 
 namespace {
@@ -155,6 +161,31 @@ hipError_t set_lds_limits(int bytes) {
     return hipSuccess;
 }
 
+// A sampling launch and the resolving launch after it, on the stream (the call parity alternates the list's count).
+spx_status run_sampling(spx_sampler * s, spx::Launch & a, void * stream) {
+    a.parity = s->parity;
+    s->parity ^= 1;
+    hipError_t e = launch_sampler(a, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
+    // the rows the sampling kernel left, resolved by a work-group each (a launch that finds none ends at once)
+    spx::Launch r;
+    plan_resolve(r, a, s->max_hist);
+    e = launch_resolver(r, std::min(a.rows, s->cus), (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "resolve_kernel launch");
+    return SPX_OK;
+}
+
+// The common part of a sampling call's launch record.
+void fill_launch(spx::Launch & a, const void * logits, int dtype, int rows, int vocab, int64_t ld) {
+    a.logits = logits;
+    a.ld = ld;
+    a.rows = rows;
+    a.vocab = vocab;
+    a.dtype = dtype;
+    const size_t esz = dtype == SPX_BF16 ? 2 : 4;
+    a.vec_ok = ((uintptr_t) logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
+}
+
 }  // namespace
 
 extern "C" {
@@ -208,7 +239,8 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
     const size_t n_fb = 256;
     const size_t n_pending = align_up((size_t) max_rows * sizeof(Pending), 256);
-    const size_t bytes = n_counters + n_partials + n_cands + n_fb + n_pending;
+    const size_t n_pair = align_up((size_t) max_rows * (sizeof(spx_row_params) + 8 + 3 * 4), 256) + 256;
+    const size_t bytes = n_counters + n_partials + n_cands + n_fb + n_pending + n_pair;
     e = hipMalloc(&s->ws, bytes);
     if (e != hipSuccess) {
         delete s;
@@ -232,6 +264,19 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     s->base.pend_ctr = (uint32_t *) (p + 64);
     p += n_fb;
     s->base.pending = (Pending *) p;
+    p += n_pending;
+    s->pair_params = (spx_row_params *) p;
+    p += (size_t) max_rows * sizeof(spx_row_params);
+    s->pair_u = (double *) p;
+    p += (size_t) max_rows * 8;
+    s->pair_map = (int32_t *) p;
+    s->pair_ids = s->pair_map + max_rows;
+    s->pair_status = s->pair_ids + max_rows;
+    s->base.row_map = nullptr;
+    s->base.hist_stride = 0;
+    s->base.hist_first = s->base.hist_len = 0;
+    s->base.u_stride = 1;
+    s->base.out_stride = 1;
     s->base.max_hist = max_hist;
     *out = s;
     return SPX_OK;
@@ -257,13 +302,7 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     if (d_out_cand_ids && s->max_out <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "the handle was created with max_out 0");
     if (rows == 0) return SPX_OK;
     spx::Launch a = s->base;
-    a.logits = d_logits;
-    a.ld = ld;
-    a.rows = rows;
-    a.vocab = vocab;
-    a.dtype = dtype;
-    const size_t esz = dtype == SPX_BF16 ? 2 : 4;
-    a.vec_ok = ((uintptr_t) d_logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
+    fill_launch(a, d_logits, dtype, rows, vocab, ld);
     a.hist = d_hist;
     a.hist_off = d_hist_off;
     a.banned = d_banned;
@@ -277,16 +316,7 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
     a.out_cand_w = d_out_cand_weights;
     a.max_out = d_out_cand_ids ? s->max_out : 0;
     plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
-    a.parity = s->parity;
-    s->parity ^= 1;
-    hipError_t e = launch_sampler(a, (hipStream_t) stream);
-    if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
-    // the rows the sampling kernel left, resolved by a work-group each (a launch that finds none ends at once)
-    spx::Launch r;
-    plan_resolve(r, a, s->max_hist);
-    e = launch_resolver(r, std::min(rows, s->cus), (hipStream_t) stream);
-    if (e != hipSuccess) return hip_fail(e, "resolve_kernel launch");
-    return SPX_OK;
+    return run_sampling(s, a, stream);
 }
 
 spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
@@ -295,13 +325,7 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
     if (st != SPX_OK) return st;
     if (rows == 0) return SPX_OK;
     spx::Launch a = s->base;
-    a.logits = d_logits;
-    a.ld = ld;
-    a.rows = rows;
-    a.vocab = vocab;
-    a.dtype = dtype;
-    const size_t esz = dtype == SPX_BF16 ? 2 : 4;
-    a.vec_ok = ((uintptr_t) d_logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
+    fill_launch(a, d_logits, dtype, rows, vocab, ld);
     a.hist = nullptr;
     a.hist_off = nullptr;
     a.banned = d_banned;
@@ -318,6 +342,87 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
     hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
+}
+
+spx_status spx_talker_bans(uint32_t * d_words, int vocab, int suppressed_tokens, int32_t end_of_speech, int frames,
+                           int min_frames, void * stream) {
+    if (!d_words || vocab <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "null mask or empty vocabulary");
+    if (suppressed_tokens < 0 || suppressed_tokens > vocab) return fail(SPX_ERR_INVALID_ARGUMENT, "suppressed_tokens outside [0, vocab]");
+    if (end_of_speech < 0 || end_of_speech >= vocab) return fail(SPX_ERR_INVALID_ARGUMENT, "end_of_speech outside the vocabulary");
+    const hipError_t e = spx::launch_talker_bans(d_words, vocab, suppressed_tokens, end_of_speech, frames, min_frames,
+                                                 (hipStream_t) stream);
+    return e == hipSuccess ? SPX_OK : hip_fail(e, "talker_bans launch");
+}
+
+spx_status spx_sample_chain(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                            int32_t * d_codes, int codes_stride, int step, int picks, const spx_row_params * d_params,
+                            const double * d_u, int32_t * d_out_status, void * stream) {
+    spx_status st = check_common(s, d_logits, dtype, rows, vocab, ld, nullptr, 0, d_codes);
+    if (st != SPX_OK) return st;
+    if (rows > 0 && (!d_params || !d_u)) return fail(SPX_ERR_INVALID_ARGUMENT, "null params or u");
+    if (step < 0 || step >= picks || codes_stride < picks + 1)
+        return fail(SPX_ERR_INVALID_ARGUMENT, "step outside [0, picks) or codes_stride below picks + 1");
+    if (step > s->max_hist) return fail(SPX_ERR_INVALID_ARGUMENT, "the handle's max_hist is below the chain's picks");
+    if (rows == 0) return SPX_OK;
+    spx::Launch a = s->base;
+    fill_launch(a, d_logits, dtype, rows, vocab, ld);
+    // pick `step` reads codes 1..step of its stream as the history and writes code step + 1
+    a.hist = d_codes;
+    a.hist_off = nullptr;
+    a.hist_stride = codes_stride;
+    a.hist_first = 1;
+    a.hist_len = step;
+    a.banned = nullptr;
+    a.banned_stride = 0;
+    a.params = d_params;
+    a.u = d_u + step;
+    a.u_stride = picks;
+    a.out_ids = d_codes + step + 1;
+    a.out_stride = codes_stride;
+    a.out_status = d_out_status;
+    a.out_kept = nullptr;
+    a.out_cand_ids = nullptr;
+    a.out_cand_w = nullptr;
+    a.max_out = 0;
+    plan_launch(s, a, false, true, false);
+    return run_sampling(s, a, stream);
+}
+
+spx_status spx_drama3_main(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                           const spx_row_params * d_first, const spx_row_params * d_again, const double * d_u_first,
+                           const double * d_u_again, const int32_t * d_token_ids, int32_t semantic_begin,
+                           int32_t semantic_end, int window, const int32_t * d_hist, const int32_t * d_hist_off,
+                           int32_t * d_out_ids, int32_t * d_out_status, void * stream) {
+    spx_status st = check_common(s, d_logits, dtype, 2 * rows, vocab, ld, nullptr, 0, d_out_ids);
+    if (st != SPX_OK) return st;
+    if (rows > 0 && (!d_first || !d_again || !d_u_first || !d_u_again || !d_token_ids))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "null params, u or token ids");
+    if ((d_hist == nullptr) != (d_hist_off == nullptr)) return fail(SPX_ERR_INVALID_ARGUMENT, "hist and hist_off go together");
+    if (rows == 0) return SPX_OK;
+    hipError_t e = spx::launch_pair_prep(rows, d_first, d_again, d_u_first, d_u_again, s->pair_params, s->pair_u,
+                                         s->pair_map, (hipStream_t) stream);
+    if (e != hipSuccess) return hip_fail(e, "pair_prep launch");
+    spx::Launch a = s->base;
+    fill_launch(a, d_logits, dtype, 2 * rows, vocab, ld);
+    a.row_map = s->pair_map;
+    a.hist = nullptr;
+    a.hist_off = nullptr;
+    a.banned = nullptr;
+    a.banned_stride = 0;
+    a.params = s->pair_params;
+    a.u = s->pair_u;
+    a.out_ids = s->pair_ids;
+    a.out_status = s->pair_status;
+    a.out_kept = nullptr;
+    a.out_cand_ids = nullptr;
+    a.out_cand_w = nullptr;
+    a.max_out = 0;
+    plan_launch(s, a, false, false, false);
+    st = run_sampling(s, a, stream);
+    if (st != SPX_OK) return st;
+    e = spx::launch_pair_pick(rows, s->pair_ids, s->pair_status, d_token_ids, semantic_begin, semantic_end, window,
+                              d_hist, d_hist_off, d_out_ids, d_out_status, (hipStream_t) stream);
+    return e == hipSuccess ? SPX_OK : hip_fail(e, "pair_pick launch");
 }
 
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {

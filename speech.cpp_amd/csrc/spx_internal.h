@@ -118,6 +118,13 @@ struct Launch {
     Partial * partials;    // [max_rows * kMaxSplitsGreedy]
     uint64_t * part_cands; // [max_rows * kMaxSplits * kKeep]
     int32_t * fb_count;    // rows resolved past the one-pass path since the handle was made
+    // Row addressing beyond the dense layout (the device chain and the two-draw entries): the logits row each sampled
+    // row reads (null: its own), a strided history (row r's ids at hist[r * hist_stride + hist_first], hist_len of
+    // them, where hist_off is null), and strides of the uniforms and of the ids written.
+    const int32_t * row_map;
+    int64_t hist_stride;
+    int hist_first, hist_len;
+    int64_t u_stride, out_stride;
     Pending * pending;     // [max_rows]: the rows left to the resolving kernel
     uint32_t * pend_ctr;   // [4]: the count of rows left and of rows taken, one of each per call parity
     int parity;            // this call's slot of pend_ctr: calls alternate, so that no kernel has to clear its own
@@ -139,6 +146,15 @@ hipError_t resolve_f32_1024(const Launch & a, int grid, hipStream_t s);
 hipError_t resolve_bf16_1024(const Launch & a, int grid, hipStream_t s);
 hipError_t resolve_f32_256(const Launch & a, int grid, hipStream_t s);
 hipError_t resolve_bf16_256(const Launch & a, int grid, hipStream_t s);
+// The kernels of spx_aux.hip.
+hipError_t launch_talker_bans(uint32_t * words, int vocab, int suppressed, int32_t eos, int frames, int min_frames,
+                              hipStream_t s);
+hipError_t launch_pair_prep(int rows, const spx_row_params * first, const spx_row_params * again, const double * u_first,
+                            const double * u_again, spx_row_params * params, double * u, int32_t * row_map,
+                            hipStream_t s);
+hipError_t launch_pair_pick(int rows, const int32_t * ids, const int32_t * status, const int32_t * token_ids,
+                            int32_t sem_lo, int32_t sem_hi, int window, const int32_t * hist, const int32_t * hist_off,
+                            int32_t * out_ids, int32_t * out_status, hipStream_t s);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);
 hipError_t lds_limit_f32_256(int bytes);

@@ -283,12 +283,25 @@ struct Elt<uint16_t> {
     static constexpr int U = 2;
 };
 
+// The logits row a sampled row reads.
+__device__ __forceinline__ int64_t logits_row(const Launch & a, int row) { return a.row_map ? a.row_map[row] : row; }
+
+// Row r's history range [h0, h1) of the ids: from the offsets, or strided (see Launch).
+__device__ __forceinline__ void hist_bounds(const Launch & a, int row, int & h0, int & h1) {
+    if (a.hist_off) {
+        h0 = a.hist_off[row];
+        h1 = a.hist_off[row + 1];
+    } else {
+        h0 = (int) ((int64_t) row * a.hist_stride) + a.hist_first;
+        h1 = h0 + a.hist_len;
+    }
+}
+
 // The row's history range [h0, h1) of the concatenated ids; flags a history longer than the handle takes.
 __device__ __forceinline__ void hist_range(const Launch & a, int row, const Plan & pl, int & h0, int & h1, uint32_t & bad) {
     h0 = h1 = 0;
     if (!pl.pen) return;
-    h0 = a.hist_off[row];
-    h1 = a.hist_off[row + 1];
+    hist_bounds(a, row, h0, h1);
     if (h1 - h0 > a.max_hist || h1 < h0) {
         bad |= kBadHist;
         h1 = h0;
@@ -915,7 +928,7 @@ __device__ __forceinline__ int row_status(const Plan & pl, const spx_row_params 
 }
 
 __device__ __forceinline__ void write_row(const Launch & a, int row, int id, int status, int kept) {
-    a.out_ids[row] = status == SPX_ROW_OK ? id : -1;
+    a.out_ids[(int64_t) row * a.out_stride] = status == SPX_ROW_OK ? id : -1;
     if (a.out_status) a.out_status[row] = status;
     if (a.out_kept) a.out_kept[row] = status == SPX_ROW_OK ? kept : 0;
 }
@@ -964,7 +977,7 @@ __device__ __forceinline__ double wave_sum4(const double (&x)[4]) { return wave_
 __device__ __forceinline__ bool finish_wave(const Launch & a, int row, const spx_row_params & p, const Plan & pl,
                                    const RowTotals & tot, const uint64_t * e, int n, bool complete, float * pf) {
     const int lane = lane_id();
-    const double u = a.u ? a.u[row] : 0.0;
+    const double u = a.u ? a.u[(int64_t) row * a.u_stride] : 0.0;
     const float top = n > 0 ? entry_value(e[0]) : -INFINITY;
     const int st = row_status(pl, p, tot.flags, n > 0 && __builtin_isfinite(top));
     if (st >= 0) {
@@ -1294,7 +1307,7 @@ template <typename T, int B, typename F>
 __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
     constexpr int V = Elt<T>::V, U = Elt<T>::U;
     const Launch & a = *r.a;
-    const T * rowp = (const T *) a.logits + (int64_t) r.row * a.ld;
+    const T * rowp = (const T *) a.logits + logits_row(a, r.row) * a.ld;
     const bool spec = r.pl.pen || r.banned_row;
     const uint32_t ninf = order_key(-INFINITY);
     const int tid = threadIdx.x;
@@ -1497,7 +1510,7 @@ __device__ __forceinline__ void fallback_row(const Launch & a, int row, const sp
     __syncthreads();
     const uint64_t all_m = *tot_m;
     __syncthreads();
-    const double u = a.u[row];
+    const double u = a.u[(int64_t) row * a.u_stride];
     const int fl_ = pl.flavor;
     auto sel = [&](bool by_mass, uint64_t target, bool strict, Select & out) {
         return fb_select<T, B>(r, by_mass, target, strict, out, hist_n, hist_m);
@@ -1824,7 +1837,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
     // The zeroing, the weights' double sum, the listed candidates; then the pick. One lane keeps the state in LDS.
     const float tp = pl.top_p;
     const float stop_at = __uint_as_float(__float_as_uint(tp) + 2u);
-    const double u = a.u[row];
+    const double u = a.u[(int64_t) row * a.u_stride];
     const int nl = a.out_cand_ids ? (int) min((uint64_t) a.max_out, k) : 0;
     double * dsh = (double *) &m.red[4];
     uint64_t * ush = &m.red[8];
@@ -2020,7 +2033,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
     // src/families/haru/sampler.cpp:36-59, src/families/drama3/sampler.cpp:44-59 and src/common/sampling.cpp:9-19).
     const int fl = pl.flavor;
     const uint64_t k = (uint64_t) pl.k;
-    const double u = a.u[row];
+    const double u = a.u[(int64_t) row * a.u_stride];
     WideQ q[kWideQs];
     for (int i = 0; i < kWideQs; i++) {
         q[i].kind = kQNone;
@@ -2943,14 +2956,11 @@ __global__ __launch_bounds__(B, 4) void sampler_kernel(Launch a) {
     xcd_map((int) blockIdx.x, a.nwg, a.splits, row, split);
     if (row >= a.rows) return;
     const int c0 = split * a.chunk, c1 = min(a.vocab, c0 + a.chunk);
-    const T * rowp = (const T *) a.logits + (int64_t) row * a.ld;
+    const T * rowp = (const T *) a.logits + logits_row(a, row) * a.ld;
     // The row's history offsets and parameters are requested first (they need only the row), then the first step's
     // logits, then the history ids once their offsets are in; the special tokens are built once those are in.
     int h0 = 0, h1 = 0;
-    if (a.hist) {
-        h0 = a.hist_off[row];
-        h1 = a.hist_off[row + 1];
-    }
+    if (a.hist) hist_bounds(a, row, h0, h1);
     spx_row_params p;
     if (a.params) {
         p = a.params[row];

@@ -48,6 +48,11 @@ def oracle():
         lib.orc_sample_rows.restype = None
         lib.orc_final_logits.argtypes = [vp, i32, vp, vp, i32, vp, vp]
         lib.orc_final_logits.restype = i32
+        lib.orc_talker_bans.argtypes = [i32, i32, i32, i32, i32, vp]
+        lib.orc_talker_bans.restype = None
+        lib.orc_drama3_main.argtypes = [vp, i32, vp, vp, ctypes.c_double, ctypes.c_double, vp, i32, i32, i32, vp, i32,
+                                        vp]
+        lib.orc_drama3_main.restype = i32
         _oracle = lib
     return _oracle
 
@@ -135,3 +140,23 @@ def sample_rows(w, threads=8, cap=0):
                              _ptr(w["banned"]), w["banned_stride"], _ptr(np.ascontiguousarray(w["params"])),
                              _ptr(w["u"]), _ptr(reports), _ptr(cids), _ptr(cweights), cap, threads)
     return reports, cids, cweights
+
+
+def talker_bans(vocab, suppressed_tokens, end_of_speech, frames, min_frames):
+    """Generation::banned as a 0/1 array of vocab entries."""
+    out = np.zeros(vocab, dtype=np.uint8)
+    oracle().orc_talker_bans(vocab, suppressed_tokens, end_of_speech, frames, min_frames, _ptr(out))
+    return out
+
+
+def drama3_main(logits, first, again, u_first, u_again, token_ids, semantic_begin, semantic_end, window, history):
+    """FrameSampler::main: (status, text-model id)."""
+    l = np.ascontiguousarray(logits, dtype=np.float32)
+    f = np.ascontiguousarray(first)
+    g = np.ascontiguousarray(again)
+    t = np.ascontiguousarray(token_ids, dtype=np.int32)
+    h = np.ascontiguousarray(history if history is not None else np.zeros(0), dtype=np.int32)
+    out = np.full(1, -7, dtype=np.int32)
+    st = oracle().orc_drama3_main(_ptr(l), len(l), _ptr(f), _ptr(g), u_first, u_again, _ptr(t), semantic_begin,
+                                  semantic_end, window, _ptr(h), len(h), _ptr(out))
+    return st, int(out[0])
