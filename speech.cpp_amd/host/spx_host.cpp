@@ -9,18 +9,34 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdio>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
+#include <stdexcept>
 
 #include "../../include/spx_sampler.h"
 
 namespace spx_host {
 namespace {
 
+// A float in an error message as the reference writes it (src/common/json.h:39-63, json_number of a float): the
+// shortest %g that reads back as the same float, in fixed notation where %g would take an exponent for a magnitude
+// from 1e-4 to below 1e17; "null" for infinities and NaN.
 std::string number(float v) {
-    char b[32];
-    std::snprintf(b, sizeof b, "%.9g", (double) v);
+    if (!std::isfinite(v)) return "null";
+    char b[64];
+    for (int precision = 1; precision <= 9; precision++) {
+        std::snprintf(b, sizeof b, "%.*g", precision, (double) v);
+        if (std::strtof(b, nullptr) == v) break;
+    }
+    const double magnitude = std::fabs((double) v);
+    if (std::strchr(b, 'e') && magnitude >= 1e-4 && magnitude < 1e17) {
+        for (int decimals = 0; decimals <= 20; decimals++) {
+            std::snprintf(b, sizeof b, "%.*f", decimals, (double) v);
+            if (std::strtof(b, nullptr) == v) break;
+        }
+    }
     return b;
 }
 
@@ -259,6 +275,89 @@ int32_t argmax(const std::vector<float> & logits, const std::vector<bool> & bann
     return row.id;
 }
 
+std::vector<bool> Generation::banned(int vocab, int32_t end_of_speech, int frames) const {
+    std::vector<bool> b((size_t) vocab, false);
+    for (int i = std::max(0, vocab - suppressed_tokens); i < vocab; i++) b[(size_t) i] = i != end_of_speech;
+    if (frames < min_frames) b[(size_t) end_of_speech] = true;
+    return b;
+}
+
+// The chain's device buffers: the sampler, the codes (streams x (picks + 1)), the numbers, the settings, the statuses.
+struct GraphSampler::Device {
+    spx_sampler * handle = nullptr;
+    void * base = nullptr;
+    int32_t * codes = nullptr;
+    double * u = nullptr;
+    spx_row_params * params = nullptr;
+    int32_t * status = nullptr;
+    void * last_stream = nullptr;
+};
+
+bool GraphSampler::follows(const SamplingParams & p) { return p.greedy || (p.temperature > 0.0f && std::isfinite(p.temperature)); }
+
+GraphSampler::GraphSampler(const SamplingParams & p, int vocab, int picks, int streams)
+    : p_(p), vocab_(vocab), picks_(picks), streams_(streams), d_(new Device()) {
+    if (!follows(p)) throw std::logic_error("the chain cannot pick under a temperature that is not a positive number");
+    check_spx(spx_sampler_create(&d_->handle, streams, vocab, picks, 0));
+    const size_t bytes = (size_t) streams * ((picks + 1) * 4 + picks * 8 + sizeof(spx_row_params) + 4) + 256;
+    check_hip(hipMalloc(&d_->base, bytes), "hipMalloc");
+    char * q = (char *) d_->base;
+    d_->u = (double *) q;
+    q += (size_t) streams * picks * 8;
+    d_->params = (spx_row_params *) q;
+    q += (size_t) streams * sizeof(spx_row_params);
+    d_->codes = (int32_t *) q;
+    q += (size_t) streams * (picks + 1) * 4;
+    d_->status = (int32_t *) q;
+    std::vector<spx_row_params> rp((size_t) streams, transformers_params(p, ExtraPenalties{}));
+    check_hip(hipMemcpy(d_->params, rp.data(), rp.size() * sizeof(spx_row_params), hipMemcpyHostToDevice), "copy params");
+    std::vector<double> zero((size_t) streams * picks, 0.0);
+    check_hip(hipMemcpy(d_->u, zero.data(), zero.size() * 8, hipMemcpyHostToDevice), "copy u");
+}
+
+GraphSampler::~GraphSampler() {
+    if (d_->base) (void) hipFree(d_->base);
+    spx_sampler_destroy(d_->handle);
+    delete d_;
+}
+
+void GraphSampler::start(const std::vector<int32_t> & first_codes) {
+    if ((int) first_codes.size() != streams_) throw std::logic_error("a frame was started with another count of streams");
+    std::vector<int32_t> frame((size_t) streams_ * (picks_ + 1), -1);
+    for (int r = 0; r < streams_; r++) frame[(size_t) r * (picks_ + 1)] = first_codes[(size_t) r];
+    check_hip(hipMemcpy(d_->codes, frame.data(), frame.size() * 4, hipMemcpyHostToDevice), "copy codes");
+}
+
+void GraphSampler::draw(const std::vector<double> & u) {
+    // src/families/qwen3-tts/graph-sampler.cpp:62-73
+    if (p_.greedy) {
+        if (!u.empty()) throw std::logic_error("greedy picks were given numbers to draw with");
+        return;
+    }
+    if ((int) u.size() != picks_ * streams_) throw std::logic_error("picks in a chain were given another count of numbers to draw with");
+    check_hip(hipMemcpy(d_->u, u.data(), u.size() * 8, hipMemcpyHostToDevice), "copy u");
+}
+
+void GraphSampler::pick(int i, const float * d_logits, void * stream) {
+    if (i < 0 || i >= picks_) throw std::logic_error("a pick outside the chain's picks");
+    check_spx(spx_sample_chain(d_->handle, d_logits, SPX_F32, streams_, vocab_, vocab_, d_->codes, picks_ + 1, i, picks_,
+                               d_->params, d_->u, d_->status, stream));
+    d_->last_stream = stream;
+}
+
+std::vector<int32_t> GraphSampler::read() {
+    check_hip(hipStreamSynchronize((hipStream_t) d_->last_stream), "hipStreamSynchronize");
+    std::vector<int32_t> frame((size_t) streams_ * (picks_ + 1)), status((size_t) streams_);
+    check_hip(hipMemcpy(frame.data(), d_->codes, frame.size() * 4, hipMemcpyDeviceToHost), "copy codes");
+    check_hip(hipMemcpy(status.data(), d_->status, status.size() * 4, hipMemcpyDeviceToHost), "copy status");
+    const spx_row_params rp = transformers_params(p_, ExtraPenalties{});
+    for (int32_t st : status) raise(st, SPX_FLAVOR_TRANSFORMERS, rp);
+    std::vector<int32_t> ids((size_t) streams_ * picks_);
+    for (int r = 0; r < streams_; r++)
+        for (int i = 0; i < picks_; i++) ids[(size_t) r * picks_ + i] = frame[(size_t) r * (picks_ + 1) + 1 + i];
+    return ids;
+}
+
 namespace haru {
 Candidates candidates(const std::vector<float> & logits, const Sampling & s) {
     const spx_row_params r = family_params(SPX_FLAVOR_HARU, s);
@@ -287,6 +386,58 @@ int32_t draw(const std::vector<float> & logits, const Sampling & s, double u) {
     raise(row.status, SPX_FLAVOR_FISH, r);
     return row.id;
 }
+
+FrameSampler::FrameSampler(const Sampling & request, const Sampling & repeat, int window, int32_t semantic_begin,
+                           int32_t semantic_end, std::vector<int32_t> token_ids)
+    : request_(request), repeat_(repeat), window_(window), semantic_begin_(semantic_begin), semantic_end_(semantic_end),
+      token_ids_(std::move(token_ids)) {}
+
+int32_t FrameSampler::main(const std::vector<float> & logits, const std::vector<int32_t> & history, double first,
+                           double again) const {
+    const int vocab = (int) logits.size();
+    if ((int) token_ids_.size() < vocab) throw Error(Fault::InvalidArgument, "fewer token ids than logits");
+    int device = 0;
+    check_hip(hipGetDevice(&device), "hipGetDevice");
+    thread_local std::map<int, std::unique_ptr<spx_sampler, void (*)(spx_sampler *)>> handles;
+    auto it = handles.find(device);
+    if (it == handles.end()) {
+        spx_sampler * h = nullptr;
+        check_spx(spx_sampler_create(&h, 2, std::max(vocab, 4097), 0, 0));
+        it = handles.emplace(device, std::unique_ptr<spx_sampler, void (*)(spx_sampler *)>(h, spx_sampler_destroy)).first;
+    }
+    const spx_row_params r1 = family_params(SPX_FLAVOR_FISH, request_), r2 = family_params(SPX_FLAVOR_FISH, repeat_);
+    const size_t nh = history.size();
+    const size_t bytes = (size_t) vocab * 4 * 2 + 2 * sizeof(spx_row_params) + 16 + (nh + 2) * 4 + 8 + 64;
+    void * base = nullptr;
+    check_hip(hipMalloc(&base, bytes), "hipMalloc");
+    std::unique_ptr<void, hipError_t (*)(void *)> guard(base, hipFree);
+    char * q = (char *) base;
+    auto take = [&](size_t n) { void * p = q; q += (n + 15) / 16 * 16; return p; };
+    float * d_logits = (float *) take((size_t) vocab * 4);
+    int32_t * d_ids = (int32_t *) take((size_t) vocab * 4);
+    spx_row_params * d_p = (spx_row_params *) take(2 * sizeof(spx_row_params));
+    double * d_u = (double *) take(16);
+    int32_t * d_hist = (int32_t *) take((nh + 1) * 4);
+    int32_t * d_off = (int32_t *) take(8);
+    int32_t * d_out = (int32_t *) take(8);
+    const spx_row_params ps[2] = {r1, r2};
+    const double us[2] = {first, again};
+    const int32_t off[2] = {0, (int32_t) nh};
+    check_hip(hipMemcpy(d_logits, logits.data(), (size_t) vocab * 4, hipMemcpyHostToDevice), "copy logits");
+    check_hip(hipMemcpy(d_ids, token_ids_.data(), (size_t) vocab * 4, hipMemcpyHostToDevice), "copy token ids");
+    check_hip(hipMemcpy(d_p, ps, sizeof ps, hipMemcpyHostToDevice), "copy params");
+    check_hip(hipMemcpy(d_u, us, sizeof us, hipMemcpyHostToDevice), "copy u");
+    if (nh) check_hip(hipMemcpy(d_hist, history.data(), nh * 4, hipMemcpyHostToDevice), "copy history");
+    check_hip(hipMemcpy(d_off, off, sizeof off, hipMemcpyHostToDevice), "copy offsets");
+    check_spx(spx_drama3_main(it->second.get(), d_logits, SPX_F32, 1, vocab, vocab, d_p, d_p + 1, d_u, d_u + 1, d_ids,
+                              semantic_begin_, semantic_end_, window_, d_hist, d_off, d_out, d_out + 1, nullptr));
+    int32_t out[2];
+    check_hip(hipMemcpy(out, d_out, sizeof out, hipMemcpyDeviceToHost), "copy result");
+    raise(out[1], SPX_FLAVOR_FISH, r1);
+    return out[0];
+}
+
+int32_t FrameSampler::code(const std::vector<float> & logits, double u) const { return draw(logits, request_, u); }
 }  // namespace drama3
 
 }  // namespace spx_host
@@ -298,6 +449,31 @@ int32_t draw(const std::vector<float> & logits, const Sampling & s, double u) {
 // ------------------------------------------------------------------------------------------------------------------
 
 extern "C" {
+
+// The exception the host layer throws for a row status, as (fault + 1, message, input): 0 for SPX_ROW_OK, -1 for a
+// std::runtime_error. It needs no device: the formatting of the reference's messages is checked on the host.
+int spx_host_row_error(int status, const spx_row_params * p, char * message, int message_cap, char * input,
+                       int input_cap) {
+    using namespace spx_host;
+    auto put = [](char * dst, int cap, const char * src) {
+        if (!dst || cap <= 0) return;
+        std::strncpy(dst, src, (size_t) cap - 1);
+        dst[cap - 1] = 0;
+    };
+    put(message, message_cap, "");
+    put(input, input_cap, "");
+    try {
+        raise(status, p->flavor, *p);
+        return 0;
+    } catch (const Error & e) {
+        put(message, message_cap, e.what());
+        put(input, input_cap, e.input().c_str());
+        return (int) e.fault() + 1;
+    } catch (const std::exception & e) {
+        put(message, message_cap, e.what());
+        return -1;
+    }
+}
 
 int spx_host_call(int which, const float * logits, int vocab, const spx_row_params * p, const int32_t * history,
                   int hist_len, const uint8_t * banned, int banned_len, double u, int32_t * out_id, int32_t * out_tokens,
@@ -350,6 +526,90 @@ int spx_host_call(int which, const float * logits, int vocab, const spx_row_para
         put(message, message_cap, e.what());
         return -1;
     }
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------------------------------------------------------------------
+// C surfaces of the families' classes above, for foreign-function callers and the tests; an exception is reported as
+// in spx_host_call.
+// ------------------------------------------------------------------------------------------------------------------
+
+namespace {
+
+template <typename F>
+int report(char * message, int message_cap, F && f) {
+    auto put = [&](const char * src) {
+        if (!message || message_cap <= 0) return;
+        std::strncpy(message, src, (size_t) message_cap - 1);
+        message[message_cap - 1] = 0;
+    };
+    put("");
+    try {
+        f();
+        return 0;
+    } catch (const spx_host::Error & e) {
+        put(e.what());
+        return (int) e.fault() + 1;
+    } catch (const std::exception & e) {
+        put(e.what());
+        return -1;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+void spx_host_talker_banned(int vocab, int suppressed_tokens, int32_t end_of_speech, int frames, int min_frames,
+                            uint8_t * out) {
+    spx_host::Generation g;
+    g.suppressed_tokens = suppressed_tokens;
+    g.min_frames = min_frames;
+    const std::vector<bool> b = g.banned(vocab, end_of_speech, frames);
+    for (int i = 0; i < vocab; i++) out[i] = b[(size_t) i] ? 1 : 0;
+}
+
+int spx_host_frame_main(const float * logits, int vocab, const spx_row_params * request, const spx_row_params * repeat,
+                        int window, int32_t semantic_begin, int32_t semantic_end, const int32_t * token_ids,
+                        const int32_t * history, int n_history, double first, double again, int32_t * out_id,
+                        char * message, int message_cap) {
+    return report(message, message_cap, [&] {
+        using spx_host::drama3::Sampling;
+        const spx_host::drama3::FrameSampler f(Sampling{request->temperature, request->top_k, request->top_p},
+                                               Sampling{repeat->temperature, repeat->top_k, repeat->top_p}, window,
+                                               semantic_begin, semantic_end,
+                                               std::vector<int32_t>(token_ids, token_ids + vocab));
+        *out_id = f.main(std::vector<float>(logits, logits + vocab),
+                         std::vector<int32_t>(history, history + (history ? n_history : 0)), first, again);
+    });
+}
+
+// The chain over host logits (picks x streams x vocab), each step's copied to the device before its pick.
+int spx_host_graph_chain(const float * logits, int streams, int vocab, int picks, const spx_row_params * p,
+                         const int32_t * first_codes, const double * u, int32_t * out_codes, char * message,
+                         int message_cap) {
+    return report(message, message_cap, [&] {
+        spx_host::SamplingParams sp;
+        sp.greedy = p->greedy != 0;
+        sp.temperature = p->temperature;
+        sp.top_k = p->top_k;
+        sp.top_p = p->top_p;
+        sp.repetition_penalty = p->repetition_penalty;
+        spx_host::GraphSampler g(sp, vocab, picks, streams);
+        g.start(std::vector<int32_t>(first_codes, first_codes + streams));
+        if (!sp.greedy) g.draw(std::vector<double>(u, u + (size_t) picks * streams));
+        float * d = nullptr;
+        spx_host::check_hip(hipMalloc((void **) &d, (size_t) streams * vocab * 4), "hipMalloc");
+        std::unique_ptr<void, hipError_t (*)(void *)> guard(d, hipFree);
+        for (int i = 0; i < picks; i++) {
+            spx_host::check_hip(hipMemcpy(d, logits + (size_t) i * streams * vocab, (size_t) streams * vocab * 4,
+                                hipMemcpyHostToDevice), "copy logits");
+            g.pick(i, d, nullptr);
+        }
+        const std::vector<int32_t> ids = g.read();
+        std::copy(ids.begin(), ids.end(), out_codes);
+    });
 }
 
 }  // extern "C"

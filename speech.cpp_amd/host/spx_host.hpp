@@ -10,6 +10,9 @@
 //                                  (src/families/haru/dialogue.cpp:214, src/families/drama3/sampler.cpp:70-84),
 //                                  in one device call
 //   spx_host::argmax()             std::max_element of the suppressed logits (src/families/qwen3-asr/decoder.cpp:112)
+//   spx_host::Generation::banned() src/families/qwen3-tts/sampler.h:42
+//   spx_host::GraphSampler         src/families/qwen3-tts/graph-sampler.h:18-57, the chain of picks on the device
+//   spx_host::drama3::FrameSampler src/families/drama3/sampler.h:35-61
 //
 // Errors are the reference's: Error(Fault::OutOfRange, ..., "repetition_penalty" | "temperature"),
 // Error(Fault::Device, ...) for logits that are not finite where a family refuses them, std::runtime_error where
@@ -67,6 +70,50 @@ struct ExtraPenalties {
     float frequency = 0.0f;
 };
 
+/**
+ * src/families/qwen3-tts/sampler.h:26-43 without the model file: the stacks' settings, the frame bounds and the count
+ * of suppressed ids at the end of the talker's vocabulary, which the caller reads from its file.
+ */
+struct Generation {
+    SamplingParams talker, code_predictor;
+    int min_frames = 0, max_frames = 0;
+    int suppressed_tokens = 0;
+    /** src/families/qwen3-tts/sampler.cpp:62-67 */
+    std::vector<bool> banned(int vocab, int32_t end_of_speech, int frames) const;
+};
+
+/**
+ * The code predictor's picks kept on the device (src/families/qwen3-tts/graph-sampler.h:18-57): `picks` picks per
+ * frame for `streams` streams, each from the logits of its step's head on the device, its history the frame's codes
+ * picked before it, so that a repetition penalty other than 1 stays on the device too. A frame: start() with the
+ * first codes, draw() with the frame's numbers, pick() once per step between the predictor's forwards (asynchronous on
+ * the given stream), read() for the codes.
+ */
+class GraphSampler {
+public:
+    /** Every setting the sampler takes is followed on the device, penalties included. */
+    static bool follows(const SamplingParams & p);
+    GraphSampler(const SamplingParams & p, int vocab, int picks, int streams = 1);
+    ~GraphSampler();
+    GraphSampler(const GraphSampler &) = delete;
+    GraphSampler & operator=(const GraphSampler &) = delete;
+    const SamplingParams & params() const { return p_; }
+    /** The frame's first codes (the talker's), one per stream. */
+    void start(const std::vector<int32_t> & first_codes);
+    /** The numbers of the frame's draws, picks per stream in order, stream after stream; none for greedy picks. */
+    void draw(const std::vector<double> & u);
+    /** Pick `i` from the step's logits on the device, streams x vocab float32, on `stream` (a hipStream_t). */
+    void pick(int i, const float * d_logits, void * stream);
+    /** The codes of the frame, picks per stream, stream after stream; throws as candidates() does. */
+    std::vector<int32_t> read();
+
+private:
+    SamplingParams p_;
+    int vocab_, picks_, streams_;
+    struct Device;
+    Device * d_;
+};
+
 Candidates candidates(const std::vector<float> & logits, const SamplingParams & p, const std::vector<int32_t> & history,
                       const std::vector<bool> & banned);
 int32_t sample(const std::vector<float> & logits, const SamplingParams & p, const std::vector<int32_t> & history,
@@ -95,6 +142,28 @@ struct Sampling {
 };
 Candidates candidates(const std::vector<float> & logits, const Sampling & s);
 int32_t draw(const std::vector<float> & logits, const Sampling & s, double u);
+
+/**
+ * src/families/drama3/sampler.h:35-61 without the model file: the request's settings, the redraw's, its window, the
+ * semantic id range and the map from the output's logits to text-model ids, which the caller reads from its file.
+ */
+class FrameSampler {
+public:
+    FrameSampler(const Sampling & request, const Sampling & repeat, int window, int32_t semantic_begin,
+                 int32_t semantic_end, std::vector<int32_t> token_ids);
+    /** src/families/drama3/sampler.cpp:70-79, both draws and the redraw rule in one device call */
+    int32_t main(const std::vector<float> & logits, const std::vector<int32_t> & history, double first,
+                 double again) const;
+    /** src/families/drama3/sampler.cpp:81-84 */
+    int32_t code(const std::vector<float> & logits, double u) const;
+    bool semantic(int32_t id) const { return id >= semantic_begin_ && id <= semantic_end_; }
+
+private:
+    Sampling request_, repeat_;
+    int window_;
+    int32_t semantic_begin_, semantic_end_;
+    std::vector<int32_t> token_ids_;
+};
 }  // namespace drama3
 
 }  // namespace spx_host

@@ -29,6 +29,8 @@ PICK_CASES = [
     ([1e-300, 1.0, 1e300], [0.0, 0.5, 1.0]),
     ([0.1] * 10, [0.1, 0.2, 0.3, 0.30000000000000004, 0.7, 0.99]),
 ]
+# temperature_overflow()'s message (src/common/sampling.cpp:21-25) is kept for these temperatures
+TEMPERATURES = [1e-38, 0.7, 1e-5, 3e-45, 123456.0, 1e20, 0.1, 2.5e-4, float("inf")]
 # (workload, rows, seed)
 WORKLOADS = [("talker", 1, 1234), ("predictor", 32, 1234), ("asr", 4, 1234), ("haru", 4, 1234), ("mixed", 16, 1234)]
 NCAND = 8
@@ -57,9 +59,16 @@ def reference_fixture():
             picks.append(oracle_lib.ref().ref_pick(np.asarray(weights, dtype=np.float64).ctypes.data_as(
                 oracle_lib.ctypes.c_void_p), len(weights), u))
         u_off.append(len(u_flat))
+    messages = []
+    for t in TEMPERATURES:
+        msg = oracle_lib.ctypes.create_string_buffer(512)
+        inp = oracle_lib.ctypes.create_string_buffer(64)
+        oracle_lib.ref().ref_temperature_overflow(t, msg, 512, inp, 64)
+        messages.append(msg.value.decode())
     np.savez(os.path.join(HERE, "reference_sampling.npz"), seeds=np.array(SEEDS, dtype=np.uint64), uniform=uni,
              weights=np.array(w_flat), weight_off=np.array(w_off), u=np.array(u_flat), u_off=np.array(u_off),
-             pick=np.array(picks, dtype=np.int32))
+             pick=np.array(picks, dtype=np.int32), temperatures=np.array(TEMPERATURES, dtype=np.float32),
+             temperature_messages=np.array(messages))
     print("wrote reference_sampling.npz")
 
 

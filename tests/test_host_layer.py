@@ -157,3 +157,107 @@ def test_exceptions_are_the_references():
     params = spx.row_params(1, spx.TRANSFORMERS, temperature=0.9, top_k=50)[0]
     rc, _, _, _, msg, _ = call(SAMPLE, logits, params, banned=np.ones(3072, dtype=np.uint8))
     assert rc == RUNTIME_ERROR and "finite" in msg
+
+
+def row_error(status, params):
+    lib = host()
+    lib.spx_host_row_error.argtypes = [ctypes.c_int, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int, ctypes.c_char_p,
+                                       ctypes.c_int]
+    lib.spx_host_row_error.restype = ctypes.c_int
+    msg = ctypes.create_string_buffer(512)
+    inp = ctypes.create_string_buffer(64)
+    p = np.ascontiguousarray(params)
+    rc = lib.spx_host_row_error(status, p.ctypes.data_as(ctypes.c_void_p), msg, 512, inp, 64)
+    return rc, msg.value.decode(), inp.value.decode()
+
+
+def test_error_messages_are_the_references():
+    # temperature_overflow() (src/common/sampling.cpp:21-25) writes the temperature as json_number() does, the
+    # shortest decimal that reads back as the float (src/common/json.h:39-63): the host layer's message must be the
+    # reference's, word for word, as the reference's compiled sampling.cpp wrote it into the golden fixture.
+    spx = workloads.spx_module()
+    g = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "reference_sampling.npz"))
+    for t, want in zip(g["temperatures"].tolist(), g["temperature_messages"].tolist()):
+        p = spx.row_params(1, spx.TRANSFORMERS, temperature=t)[0]
+        rc, msg, inp = row_error(spx.ROW_TEMPERATURE_OVERFLOW, p)
+        assert (rc, inp) == (OUT_OF_RANGE, "temperature")
+        assert msg == want
+        if oracle_lib.ref() is not None:
+            m2 = ctypes.create_string_buffer(512)
+            i2 = ctypes.create_string_buffer(64)
+            oracle_lib.ref().ref_temperature_overflow(np.float32(t), m2, 512, i2, 64)
+            assert msg == m2.value.decode()
+    # the repetition penalty's message (src/families/qwen3-tts/sampler.cpp:44-48) writes its penalty the same way
+    p = spx.row_params(1, spx.TRANSFORMERS, repetition_penalty=1e-40)[0]
+    rc, msg, inp = row_error(spx.ROW_REP_PENALTY_OVERFLOW, p)
+    assert (rc, inp) == (OUT_OF_RANGE, "repetition_penalty")
+    assert msg.startswith("the repetition penalty 1e-40 pushes a logit beyond the range of a float")
+    rc, msg, _ = row_error(spx.ROW_NO_FINITE_LOGIT, p)
+    assert rc == RUNTIME_ERROR and msg == "no token has a finite logit to pick from"
+
+
+def test_generation_banned_is_the_oracles():
+    lib = host()
+    lib.spx_host_talker_banned.argtypes = [ctypes.c_int] * 5 + [ctypes.c_void_p]
+    lib.spx_host_talker_banned.restype = None
+    for vocab, sup, eos, frames, min_frames in ((3072, 1024, 2150, 0, 2), (3072, 1024, 2150, 9, 2), (3072, 1024, 5, 1, 3)):
+        out = np.zeros(vocab, dtype=np.uint8)
+        lib.spx_host_talker_banned(vocab, sup, eos, frames, min_frames, out.ctypes.data_as(ctypes.c_void_p))
+        np.testing.assert_array_equal(out, oracle_lib.talker_bans(vocab, sup, eos, frames, min_frames))
+
+
+@pytest.mark.gpu
+def test_frame_sampler_main_is_the_oracles():
+    spx = workloads.spx_module()
+    lib = host()
+    lib.spx_host_frame_main.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int,
+                                        ctypes.c_double, ctypes.c_double, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int]
+    lib.spx_host_frame_main.restype = ctypes.c_int
+    rng = np.random.default_rng(53)
+    vocab, window = 4097, 8
+    token_ids = rng.permutation(np.arange(151000, 151000 + vocab)).astype(np.int32)
+    request = spx.row_params(1, spx.FISH, temperature=0.8, top_k=30, top_p=0.9)[0]
+    repeat = spx.row_params(1, spx.FISH, temperature=1.0, top_k=50, top_p=0.95)[0]
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    for trial in range(12):
+        logits = distinct_logits(rng, vocab)
+        top = token_ids[np.argsort(-logits)[:2]]
+        history = np.concatenate([rng.integers(151000, 151000 + vocab, 10), top[: trial % 3]]).astype(np.int32)
+        u1, u2 = float(rng.random()), float(rng.random())
+        out = np.full(1, -7, dtype=np.int32)
+        msg = ctypes.create_string_buffer(256)
+        rc = lib.spx_host_frame_main(ptr(logits), vocab, ptr(np.ascontiguousarray(request)),
+                                     ptr(np.ascontiguousarray(repeat)), window, 151005, 151000 + vocab - 1,
+                                     ptr(token_ids), ptr(history), len(history), u1, u2, ptr(out), msg, 256)
+        assert rc == 0, msg.value
+        st, want = oracle_lib.drama3_main(logits, request, repeat, u1, u2, token_ids, 151005, 151000 + vocab - 1,
+                                          window, history)
+        assert st == 0 and out[0] == want, trial
+
+
+@pytest.mark.gpu
+def test_graph_sampler_chain_is_the_oracles():
+    spx = workloads.spx_module()
+    lib = host()
+    lib.spx_host_graph_chain.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                         ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_char_p, ctypes.c_int]
+    lib.spx_host_graph_chain.restype = ctypes.c_int
+    rng = np.random.default_rng(55)
+    streams, picks, vocab = 4, 15, 2048
+    logits = np.stack([np.stack([distinct_logits(rng, vocab) for _ in range(streams)]) for _ in range(picks)])
+    p = spx.row_params(1, spx.TRANSFORMERS, temperature=0.9, top_k=50, top_p=1.0, repetition_penalty=1.05)[0]
+    first = rng.integers(0, 3072, streams).astype(np.int32)
+    u = rng.uniform(0.02, 0.98, streams * picks)
+    out = np.full(streams * picks, -7, dtype=np.int32)
+    msg = ctypes.create_string_buffer(256)
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rc = lib.spx_host_graph_chain(ptr(np.ascontiguousarray(logits)), streams, vocab, picks,
+                                  ptr(np.ascontiguousarray(p)), ptr(first), ptr(u), ptr(out), msg, 256)
+    assert rc == 0, msg.value
+    got = out.reshape(streams, picks)
+    for r in range(streams):
+        for i in range(picks):
+            st, toks, wts = oracle_lib.tf_candidates(logits[i, r], p, got[r, :i], None)
+            assert st == 0
+            assert got[r, i] == toks[oracle_lib.pick(wts, u[r * picks + i])], (r, i)
