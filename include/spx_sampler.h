@@ -127,6 +127,21 @@ spx_status spx_sample_rows(spx_sampler * s, const void * d_logits, int dtype, in
                            int32_t * d_out_cand_ids, double * d_out_cand_weights, void * stream);
 
 /*
+ * The candidates of `rows` rows, every one of them: the reference's Candidates (src/common/sampling.h:10-13) of
+ *   candidates(logits, p, history, banned)   src/families/qwen3-tts/sampler.cpp:69-101 (TRANSFORMERS)
+ *   haru::candidates(logits, s)              src/families/haru/sampler.cpp:18-61 (HARU)
+ *   drama3::candidates(logits, s)            src/families/drama3/sampler.cpp:30-60 (FISH)
+ * as the first min(n, cap) tokens by falling logit and their weights (as d_out_cand_weights of spx_sample_rows
+ * describes them), -1 and 0 past them, rows x cap each; d_out_n gets n, the list's full length (up to vocab: a cap of
+ * vocab lists them all). Same layout rules as spx_sample_rows; greedy rows list their one token. A long list is read
+ * in order by batches of the row, so it costs reads of the row in proportion to its length.
+ */
+spx_status spx_candidates_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                               const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
+                               int64_t banned_stride, const spx_row_params * d_params, int cap, int32_t * d_out_tokens,
+                               double * d_out_weights, int32_t * d_out_n, int32_t * d_out_status, void * stream);
+
+/*
  * Greedy argmax of `rows` rows with a shared or per-row suppress mask: the first largest logit, NaN ignored except in
  * the first position, as std::max_element does (src/families/qwen3-asr/decoder.cpp:112,
  * src/common/qwen3-decoder.cpp:427-429 with the fork's first-of-equals argmax). Same layout rules as spx_sample_rows.

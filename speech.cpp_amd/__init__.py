@@ -30,7 +30,8 @@ ROW_PARAMS = np.dtype([("flavor", "<i4"), ("greedy", "<i4"), ("temperature", "<f
 assert ROW_PARAMS.itemsize == 32
 
 # Every symbol include/spx_sampler.h declares.
-EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_sample_chain",
+EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_candidates_rows",
+           "spx_sample_chain",
            "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats"]
 
 
@@ -62,6 +63,8 @@ def load_library(path=LIB_PATH):
     lib.spx_sample_rows.restype = i32
     lib.spx_argmax_rows.argtypes = [p, vp, i32, i32, i32, i64, vp, i64, vp, vp]
     lib.spx_argmax_rows.restype = i32
+    lib.spx_candidates_rows.argtypes = [p, vp, i32, i32, i32, i64, vp, vp, vp, i64, vp, i32, vp, vp, vp, vp, vp]
+    lib.spx_candidates_rows.restype = i32
     lib.spx_sample_chain.argtypes = [p, vp, i32, i32, i32, i64, vp, i32, i32, i32, vp, vp, vp, vp]
     lib.spx_sample_chain.restype = i32
     lib.spx_drama3_main.argtypes = [p, vp, i32, i32, i32, i64, vp, vp, vp, vp, vp, i32, i32, i32, vp, vp, vp, vp, vp]
@@ -166,6 +169,24 @@ class Sampler:
         self._check(self.lib.spx_argmax_rows(self.handle, _ptr(logits), dtype, rows, vocab, ld,
                                              _ptr(banned), banned_stride, _ptr(out_ids), ctypes.c_void_p(s)))
         return out_ids
+
+    def candidates_rows(self, logits, params, cap, hist=None, hist_off=None, banned=None, banned_stride=0,
+                        stream=None):
+        """Every row's candidates, the first `cap`: (tokens rows x cap int32, weights rows x cap float64, n, status)."""
+        import torch
+        rows, vocab = logits.shape
+        dev = logits.device
+        dtype = BF16 if logits.dtype == torch.bfloat16 else F32
+        ld = logits.stride(0) if rows > 1 else vocab
+        toks = torch.empty((rows, cap), dtype=torch.int32, device=dev)
+        wts = torch.empty((rows, cap), dtype=torch.float64, device=dev)
+        n = torch.empty(rows, dtype=torch.int32, device=dev)
+        status = torch.empty(rows, dtype=torch.int32, device=dev)
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        self._check(self.lib.spx_candidates_rows(self.handle, _ptr(logits), dtype, rows, vocab, ld, _ptr(hist),
+                                                 _ptr(hist_off), _ptr(banned), banned_stride, _ptr(params), cap,
+                                                 _ptr(toks), _ptr(wts), _ptr(n), _ptr(status), ctypes.c_void_p(s)))
+        return toks, wts, n, status
 
     def sample_chain(self, logits, codes, step, params, u, out_status=None, stream=None):
         """Pick `step` of the code-predictor chain: logits (streams x vocab), codes (streams x >= picks + 1 int32, row

@@ -25,6 +25,7 @@ struct spx_sampler {
     int32_t * pair_map = nullptr;
     int32_t * pair_ids = nullptr;
     int32_t * pair_status = nullptr;
+    double * zero_u = nullptr;  // max_rows zeros: the numbers of a listing call, which draws nothing
 };
 
 namespace {
@@ -239,7 +240,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
     const size_t n_fb = 256;
     const size_t n_pending = align_up((size_t) max_rows * sizeof(Pending), 256);
-    const size_t n_pair = align_up((size_t) max_rows * (sizeof(spx_row_params) + 8 + 3 * 4), 256) + 256;
+    const size_t n_pair = align_up((size_t) max_rows * (sizeof(spx_row_params) + 8 + 3 * 4 + 8) + 8, 256) + 256;
     const size_t bytes = n_counters + n_partials + n_cands + n_fb + n_pending + n_pair;
     e = hipMalloc(&s->ws, bytes);
     if (e != hipSuccess) {
@@ -277,6 +278,8 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     s->base.hist_first = s->base.hist_len = 0;
     s->base.u_stride = 1;
     s->base.out_stride = 1;
+    s->base.list_all = 0;
+    s->zero_u = (double *) align_up((size_t) (s->pair_status + max_rows), 8);
     s->base.max_hist = max_hist;
     *out = s;
     return SPX_OK;
@@ -342,6 +345,37 @@ spx_status spx_argmax_rows(spx_sampler * s, const void * d_logits, int dtype, in
     hipError_t e = launch_sampler(a, (hipStream_t) stream);
     if (e != hipSuccess) return hip_fail(e, "sampler_kernel launch");
     return SPX_OK;
+}
+
+spx_status spx_candidates_rows(spx_sampler * s, const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                               const int32_t * d_hist, const int32_t * d_hist_off, const uint32_t * d_banned,
+                               int64_t banned_stride, const spx_row_params * d_params, int cap, int32_t * d_out_tokens,
+                               double * d_out_weights, int32_t * d_out_n, int32_t * d_out_status, void * stream) {
+    spx_status st = check_common(s, d_logits, dtype, rows, vocab, ld, d_banned, banned_stride, d_out_n);
+    if (st != SPX_OK) return st;
+    if (rows > 0 && (!d_params || !d_out_tokens || !d_out_weights))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "null params or candidate outputs");
+    if ((d_hist == nullptr) != (d_hist_off == nullptr)) return fail(SPX_ERR_INVALID_ARGUMENT, "hist and hist_off go together");
+    if (cap <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "cap must be positive");
+    if (rows == 0) return SPX_OK;
+    // the ids of the draws (with u = 0, unread) go to the pair area's id slots, which this call does not otherwise use
+    spx::Launch a = s->base;
+    fill_launch(a, d_logits, dtype, rows, vocab, ld);
+    a.hist = d_hist;
+    a.hist_off = d_hist_off;
+    a.banned = d_banned;
+    a.banned_stride = banned_stride;
+    a.params = d_params;
+    a.u = s->zero_u;
+    a.out_ids = s->pair_ids;
+    a.out_status = d_out_status;
+    a.out_kept = d_out_n;
+    a.out_cand_ids = d_out_tokens;
+    a.out_cand_w = d_out_weights;
+    a.max_out = cap;
+    a.list_all = 1;
+    plan_launch(s, a, false, d_hist != nullptr, d_banned != nullptr);
+    return run_sampling(s, a, stream);
 }
 
 spx_status spx_talker_bans(uint32_t * d_words, int vocab, int suppressed_tokens, int32_t end_of_speech, int frames,

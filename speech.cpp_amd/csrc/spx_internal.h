@@ -125,6 +125,7 @@ struct Launch {
     int64_t hist_stride;
     int hist_first, hist_len;
     int64_t u_stride, out_stride;
+    int list_all;          // every drawing row goes to the resolving kernel, which lists its candidates (max_out: any)
     Pending * pending;     // [max_rows]: the rows left to the resolving kernel
     uint32_t * pend_ctr;   // [4]: the count of rows left and of rows taken, one of each per call parity
     int parity;            // this call's slot of pend_ctr: calls alternate, so that no kernel has to clear its own

@@ -117,7 +117,7 @@ __device__ __forceinline__ Plan make_plan(const spx_row_params & p, int vocab, b
     pl.rt = 1.0f / pl.t;
     pl.mode = k <= kKeep ? kTopK : kFull;
     // a row listing its candidates holds at least the max_out it lists
-    pl.K = pl.mode == kTopK ? k : max(kKeepFull, max_out);
+    pl.K = pl.mode == kTopK ? k : max(kKeepFull, min(max_out, kKeep));
     pl.need_s = pl.mode == kFull || p.flavor == SPX_FLAVOR_FISH;
     return pl;
 }
@@ -2513,48 +2513,34 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
     }
     if (!a.out_cand_ids) return true;
 
-    // The listed candidates: the first min(list, max_out) tokens of the order, gathered by one more read.
+    // The listed candidates: the first min(list, max_out) tokens of the order, read in order by batches of bins (one
+    // read each; a list of up to a whole vocabulary takes as many as its tokens need).
     const uint64_t nlist = min((uint64_t) kept_out, (uint64_t) a.max_out);
     const double sk = __builtin_ldexp((double) (has_k ? q[kQK].through : total), -shift);  // the top k's mass
     for (int j = (int) nlist + tid; j < a.max_out; j += B) {
         a.out_cand_ids[(int64_t) row * a.max_out + j] = -1;
         a.out_cand_w[(int64_t) row * a.max_out + j] = 0.0;
     }
-    if (nlist == 0) return true;
-    const int bl = bin_of_rank<NB>(m.pre_cnt, nlist - 1);
-    if (m.pre_cnt[bl + 1] > (uint32_t) CAP) return false;
-    for (int i = tid; i < (NB + 1 + 31) / 32; i += B) m.need[i] = 0u;
-    __syncthreads();
-    for (int b = tid; b <= bl; b += B) atomicOr(&m.need[b >> 5], 1u << (b & 31));
-    for (int b = tid; b <= NB; b += B) m.seg[b] = b <= bl ? m.pre_cnt[b] : 0u;
-    __syncthreads();
-    fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
-        if (!e) return;
-        const bool ninf = banned || !(qq > -INFINITY);
-        const int b = ninf ? NB : wide_bin<NB>(qq, top);
-        if (b > bl) return;
-        const uint32_t pos = atomicAdd(&m.seg[b], 1u);
-        m.ent[pos] = e;
-    });
-    __syncthreads();
-    const int ng = (int) m.pre_cnt[bl + 1];
-    for (int i = tid; i < ng; i += B) {
-        const uint64_t e = m.ent[i];
-        const float qq = entry_value(e);
-        const bool ninf = !(qq > -INFINITY);
-        const int b = ninf ? NB : wide_bin<NB>(qq, top);
-        const int s0 = (int) m.pre_cnt[b], s1 = (int) m.seg[b];
-        uint32_t rho = 0;
-        for (int j = s0; j < s1; j++) rho += m.ent[j] > e ? 1u : 0u;
-        const uint64_t rank = (uint64_t) s0 + rho;
-        if (rank >= nlist) continue;
-        const double w = ninf ? 0.0 : exp((double) qq - (double) top);
-        double out;
-        if (fl == SPX_FLAVOR_TRANSFORMERS) out = w / sk;
-        else if (fl == SPX_FLAVOR_HARU) out = rank < kept_n ? (double) (haru_exp(qq, top) / haru_sum) : 0.0;
-        else out = w;
-        a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(e);
-        a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = out;
+    for (int b0 = 0; b0 <= NB && (uint64_t) m.pre_cnt[b0] < nlist;) {
+        const int b1 = batch_end(m, b0);
+        if (b1 < 0) return false;  // one bin holds more tokens than a batch takes
+        uint64_t * ord = m.mass;
+        gather_in_order<T, B>(r, m, top, b0, b1, ord);
+        const uint64_t base = m.pre_cnt[b0];
+        const int n = (int) min((uint64_t) m.pre_cnt[b1 + 1], nlist) - (int) base;
+        for (int i = tid; i < n; i += B) {
+            const uint64_t e = ord[i], rank = base + (uint64_t) i;
+            const float qq = entry_value(e);
+            const double w = qq > -INFINITY ? exp((double) qq - (double) top) : 0.0;
+            double out;
+            if (fl == SPX_FLAVOR_TRANSFORMERS) out = w / sk;
+            else if (fl == SPX_FLAVOR_HARU) out = rank < kept_n ? (double) (haru_exp(qq, top) / haru_sum) : 0.0;
+            else out = w;
+            a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(e);
+            a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = out;
+        }
+        __syncthreads();
+        b0 = b1 + 1;
     }
     return true;
 }
@@ -2798,7 +2784,7 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
 
     if (a.splits == 1) {
         RowTotals t{0ull, S, M, F};
-        if (broken || !finish_block<B>(a, row, p, pl, t, cand, ntot, complete, pf, ctl)) {
+        if (a.list_all || broken || !finish_block<B>(a, row, p, pl, t, cand, ntot, complete, pf, ctl)) {
             // the largest quotient: the sorted candidates' first, unless entries were dropped
             const float top = broken ? NAN : (ntot > 0 ? entry_value(cand[0]) : -INFINITY);
             defer_row(a, row, F, top);
@@ -2855,7 +2841,7 @@ __device__ __forceinline__ void sample_row(const Launch & a, int row, int split,
         tot = min((int) ctl->ncomp, kSortCap);
         rank_sort<B>(sorted, tot, cand);
     }
-    if (any_broken || !finish_block<B>(a, row, p, pl, t, cand, tot, all_complete, pf, ctl)) {
+    if (a.list_all || any_broken || !finish_block<B>(a, row, p, pl, t, cand, tot, all_complete, pf, ctl)) {
         const float top = any_broken ? NAN : (tot > 0 ? entry_value(cand[0]) : -INFINITY);
         defer_row(a, row, t.flags, top);
     }

@@ -54,16 +54,13 @@ void check_spx(spx_status s) {
     }
 }
 
-// The candidates the device lists per row (the C ABI's limit on max_out).
-constexpr int kListed = 256;
-
 // One device's handle, staging buffers and stream, for rows of at most `vocab` logits and `hist` history ids.
 class Workspace {
 public:
     Workspace(int device, int vocab, int hist)
-        : device_(device), vocab_(vocab), hist_(hist), listed_(std::min(vocab, kListed)) {
+        : device_(device), vocab_(vocab), hist_(hist), listed_(vocab) {
         check_hip(hipSetDevice(device), "hipSetDevice");
-        check_spx(spx_sampler_create(&handle_, 1, vocab, hist, listed_));
+        check_spx(spx_sampler_create(&handle_, 1, vocab, hist, 0));
         const size_t words = (size_t) (vocab + 31) / 32;
         const size_t bytes = (size_t) vocab * 4 + sizeof(spx_row_params) + 8 + (size_t) std::max(hist, 1) * 4 + 8 +
                              words * 4 + 3 * 4 + (size_t) listed_ * 12 + 64;
@@ -127,24 +124,28 @@ public:
                       "copy banned");
             d_banned = banned_;
         }
-        check_spx(spx_sample_rows(handle_, logits_, SPX_F32, 1, vocab, vocab, d_hist, d_hist_off, d_banned, 0, params_, u_,
-                                  out_, out_ + 1, out_ + 2, want_candidates ? cand_ids_ : nullptr,
-                                  want_candidates ? cand_w_ : nullptr, stream_));
+        // candidates() lists every kept token (the row's whole list); a draw lists none
+        if (want_candidates)
+            check_spx(spx_candidates_rows(handle_, logits_, SPX_F32, 1, vocab, vocab, d_hist, d_hist_off, d_banned, 0,
+                                          params_, vocab, cand_ids_, cand_w_, out_ + 2, out_ + 1, stream_));
+        else
+            check_spx(spx_sample_rows(handle_, logits_, SPX_F32, 1, vocab, vocab, d_hist, d_hist_off, d_banned, 0, params_,
+                                      u_, out_, out_ + 1, out_ + 2, nullptr, nullptr, stream_));
         int32_t o[3];
         check_hip(hipMemcpyAsync(o, out_, sizeof o, hipMemcpyDeviceToHost, stream_), "copy result");
         Row r;
-        if (want_candidates) {
-            r.ids.resize((size_t) listed_);
-            r.weights.resize((size_t) listed_);
-            check_hip(hipMemcpyAsync(r.ids.data(), cand_ids_, (size_t) listed_ * 4, hipMemcpyDeviceToHost, stream_),
-                      "copy ids");
-            check_hip(hipMemcpyAsync(r.weights.data(), cand_w_, (size_t) listed_ * 8, hipMemcpyDeviceToHost, stream_),
-                      "copy weights");
-        }
         check_hip(hipStreamSynchronize(stream_), "hipStreamSynchronize");
         r.id = o[0];
         r.status = o[1];
         r.kept = o[2];
+        if (want_candidates && r.status == SPX_ROW_OK) {
+            // the list's own length
+            const size_t n = (size_t) std::max(0, std::min(r.kept, listed_));
+            r.ids.resize(n);
+            r.weights.resize(n);
+            check_hip(hipMemcpy(r.ids.data(), cand_ids_, n * 4, hipMemcpyDeviceToHost), "copy ids");
+            check_hip(hipMemcpy(r.weights.data(), cand_w_, n * 8, hipMemcpyDeviceToHost), "copy weights");
+        }
         return r;
     }
 
@@ -228,16 +229,11 @@ spx_row_params family_params(int flavor, const S & s) {
     return r;
 }
 
-// The kept candidates of a row the device listed in full (at most kListed; a longer list is refused).
+// A row's Candidates as the device listed them, every kept token.
 Candidates to_candidates(const Workspace::Row & r) {
     Candidates c;
-    for (int i = 0; i < r.kept; i++) {
-        if (i >= (int) r.ids.size() || r.ids[(size_t) i] < 0)
-            throw Error(Fault::InvalidArgument, "the draw keeps " + std::to_string(r.kept) +
-                                                    " tokens, more than the device lists; sample() draws from them");
-        c.tokens.push_back(r.ids[(size_t) i]);
-        c.weights.push_back(r.weights[(size_t) i]);
-    }
+    c.tokens = r.ids;
+    c.weights = r.weights;
     return c;
 }
 
