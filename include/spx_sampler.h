@@ -205,6 +205,27 @@ typedef struct spx_stats {
 } spx_stats;
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out);
 
+/* Rows per call of spx_sample_rows_noalloc. */
+#define SPX_NOALLOC_MAX_ROWS 2048
+
+/*
+ * spx_sample_rows without a handle and without allocating: no counterpart in the reference. It is for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The arguments mean what spx_sample_rows's do; max_hist bounds every row's history (a longer one is the row's
+ * SPX_ROW_INVALID_PARAMS) and max_out (0..256) is the row stride of the candidate outputs. The workspace is a static
+ * device array of the library (about 18.4 MB per device, held until the process ends) for up to SPX_NOALLOC_MAX_ROWS
+ * rows; larger calls, and a vocab and max_hist whose launch needs more than a CU's 160 KiB of LDS, are refused with
+ * SPX_ERR_INVALID_ARGUMENT. Every call on one device shares that device's array: calls that overlap on one device
+ * (on two streams, or from two threads without ordering) race, and must be ordered by the caller. The first call on
+ * a device sets the array up and waits for its stream once.
+ */
+spx_status spx_sample_rows_noalloc(const void * d_logits, int dtype, int rows, int vocab, int64_t ld,
+                                   const int32_t * d_hist, const int32_t * d_hist_off, int max_hist,
+                                   const uint32_t * d_banned, int64_t banned_stride, const spx_row_params * d_params,
+                                   const double * d_u, int32_t * d_out_ids, int32_t * d_out_status,
+                                   int32_t * d_out_kept, int32_t * d_out_cand_ids, double * d_out_cand_weights,
+                                   int max_out, void * stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -32,7 +32,7 @@ assert ROW_PARAMS.itemsize == 32
 # Every symbol include/spx_sampler.h declares.
 EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_candidates_rows",
            "spx_sample_chain",
-           "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats"]
+           "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats", "spx_sample_rows_noalloc"]
 
 
 class SpxStats(ctypes.Structure):
@@ -75,6 +75,9 @@ def load_library(path=LIB_PATH):
     lib.spx_last_error.restype = ctypes.c_char_p
     lib.spx_sampler_last_stats.argtypes = [p, ctypes.POINTER(SpxStats)]
     lib.spx_sampler_last_stats.restype = i32
+    lib.spx_sample_rows_noalloc.argtypes = [vp, i32, i32, i32, i64, vp, vp, i32, vp, i64, vp, vp, vp, vp, vp, vp, vp,
+                                            i32, vp]
+    lib.spx_sample_rows_noalloc.restype = i32
     _lib = lib
     return lib
 

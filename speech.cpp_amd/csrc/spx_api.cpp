@@ -187,7 +187,86 @@ void fill_launch(spx::Launch & a, const void * logits, int dtype, int rows, int 
     a.vec_ok = ((uintptr_t) logits % 16 == 0) && (((size_t) ld * esz) % 16 == 0);
 }
 
+// The handle's workspace pointers over `ws` (workspace_bytes(max_rows, pairs) bytes), and its fixed launch fields.
+void carve_workspace(spx_sampler * s, void * ws, int max_rows, bool pairs) {
+    using namespace spx;
+    char * p = (char *) ws;
+    s->base.counters = (uint32_t *) p;
+    p += ws_counters(max_rows);
+    s->base.partials = (Partial *) p;
+    p += ws_partials(max_rows);
+    s->base.part_cands = (uint64_t *) p;
+    p += ws_cands(max_rows);
+    s->base.fb_count = (int32_t *) p;
+    s->base.pend_ctr = (uint32_t *) (p + 64);
+    p += kWsFb;
+    s->base.pending = (Pending *) p;
+    p += ws_pending(max_rows);
+    if (pairs) {
+        s->pair_params = (spx_row_params *) p;
+        p += (size_t) max_rows * sizeof(spx_row_params);
+        s->pair_u = (double *) p;
+        p += (size_t) max_rows * 8;
+        s->pair_map = (int32_t *) p;
+        s->pair_ids = s->pair_map + max_rows;
+        s->pair_status = s->pair_ids + max_rows;
+        s->zero_u = (double *) align_up((size_t) (s->pair_status + max_rows), 8);
+    }
+    s->base.row_map = nullptr;
+    s->base.hist_stride = 0;
+    s->base.hist_first = s->base.hist_len = 0;
+    s->base.u_stride = 1;
+    s->base.out_stride = 1;
+    s->base.list_all = 0;
+    s->base.max_hist = s->max_hist;
+}
+
 }  // namespace
+
+namespace spx {
+
+spx_status report(spx_status s, const char * msg) { return fail(s, msg); }
+spx_status report_hip(hipError_t e, const char * what) { return hip_fail(e, what); }
+
+size_t lds_bound(int max_vocab, int max_hist) {
+    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary, in either work-group
+    // size a call may take, and the resolving kernel's.
+    size_t lds_max = 0;
+    for (int block : {kBlockBig, kBlockSmall}) {
+        Launch probe{};
+        lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
+    }
+    Launch probe{}, res{};
+    probe.vocab = max_vocab;
+    return std::max(lds_max, plan_resolve(res, probe, max_hist));
+}
+
+// Handles over the no-alloc entry's workspace: host records of static storage, one per device.
+spx_sampler g_bound[kMaxDevices];
+
+spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out) {
+    if (device < 0 || device >= kMaxDevices) return fail(SPX_ERR_INVALID_ARGUMENT, "device index above the no-alloc entry's table");
+    spx_sampler * s = &g_bound[device];
+    s->device = device;
+    s->max_rows = max_rows;
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) s->cus = cus;
+    const hipError_t e = set_lds_limits(160 * 1024);
+    if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute");
+    carve_workspace(s, ws, max_rows, false);
+    s->ws = nullptr;  // not the handle's to free
+    *out = s;
+    return SPX_OK;
+}
+
+void set_call_limits(spx_sampler * s, int vocab, int max_hist, int max_out) {
+    s->max_vocab = vocab;
+    s->max_hist = max_hist;
+    s->max_out = max_out;
+    s->base.max_hist = max_hist;
+}
+
+}  // namespace spx
 
 extern "C" {
 
@@ -213,18 +292,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
         s->cus = cus;
-    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary, in either work-group
-    // size a call may take.
-    size_t lds_max = 0;
-    for (int block : {kBlockBig, kBlockSmall}) {
-        Launch probe{};
-        lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
-    }
-    {
-        Launch probe{}, res{};
-        probe.vocab = max_vocab;
-        lds_max = std::max(lds_max, plan_resolve(res, probe, max_hist));
-    }
+    const size_t lds_max = spx::lds_bound(max_vocab, max_hist);
     if (lds_max > 160 * 1024) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
@@ -235,13 +303,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
         return hip_fail(e, "hipFuncSetAttribute");
     }
     // One allocation for the workspace.
-    const size_t n_counters = align_up((size_t) max_rows * 4, 256);
-    const size_t n_partials = align_up((size_t) max_rows * kMaxSplitsGreedy * sizeof(Partial), 256);
-    const size_t n_cands = align_up((size_t) max_rows * kMaxSplits * kKeep * 8, 256);
-    const size_t n_fb = 256;
-    const size_t n_pending = align_up((size_t) max_rows * sizeof(Pending), 256);
-    const size_t n_pair = align_up((size_t) max_rows * (sizeof(spx_row_params) + 8 + 3 * 4 + 8) + 8, 256) + 256;
-    const size_t bytes = n_counters + n_partials + n_cands + n_fb + n_pending + n_pair;
+    const size_t bytes = workspace_bytes(max_rows, true);
     e = hipMalloc(&s->ws, bytes);
     if (e != hipSuccess) {
         delete s;
@@ -254,33 +316,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
         delete s;
         return hip_fail(e, "hipMemset");
     }
-    char * p = (char *) s->ws;
-    s->base.counters = (uint32_t *) p;
-    p += n_counters;
-    s->base.partials = (Partial *) p;
-    p += n_partials;
-    s->base.part_cands = (uint64_t *) p;
-    p += n_cands;
-    s->base.fb_count = (int32_t *) p;
-    s->base.pend_ctr = (uint32_t *) (p + 64);
-    p += n_fb;
-    s->base.pending = (Pending *) p;
-    p += n_pending;
-    s->pair_params = (spx_row_params *) p;
-    p += (size_t) max_rows * sizeof(spx_row_params);
-    s->pair_u = (double *) p;
-    p += (size_t) max_rows * 8;
-    s->pair_map = (int32_t *) p;
-    s->pair_ids = s->pair_map + max_rows;
-    s->pair_status = s->pair_ids + max_rows;
-    s->base.row_map = nullptr;
-    s->base.hist_stride = 0;
-    s->base.hist_first = s->base.hist_len = 0;
-    s->base.u_stride = 1;
-    s->base.out_stride = 1;
-    s->base.list_all = 0;
-    s->zero_u = (double *) align_up((size_t) (s->pair_status + max_rows), 8);
-    s->base.max_hist = max_hist;
+    carve_workspace(s, s->ws, max_rows, true);
     *out = s;
     return SPX_OK;
 }

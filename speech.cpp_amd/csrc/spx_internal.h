@@ -131,6 +131,28 @@ struct Launch {
     int parity;            // this call's slot of pend_ctr: calls alternate, so that no kernel has to clear its own
 };
 
+constexpr size_t round256(size_t x) { return (x + 255) / 256 * 256; }
+
+// The workspace of `max_rows` rows, in the order it is laid out: the rows' arrival counters, the chunks' partials and
+// published candidates, the resolved-row count with the resolving list's counts, the resolving list, and (`pairs`)
+// the records of the two-draw and listing entries.
+constexpr size_t kWsFb = 256;
+constexpr size_t ws_counters(int max_rows) { return round256((size_t) max_rows * 4); }
+constexpr size_t ws_partials(int max_rows) { return round256((size_t) max_rows * kMaxSplitsGreedy * sizeof(Partial)); }
+constexpr size_t ws_cands(int max_rows) { return round256((size_t) max_rows * kMaxSplits * kKeep * 8); }
+constexpr size_t ws_pending(int max_rows) { return round256((size_t) max_rows * sizeof(Pending)); }
+constexpr size_t ws_pairs(int max_rows) {
+    return round256((size_t) max_rows * (sizeof(spx_row_params) + 8 + 3 * 4 + 8) + 8) + 256;
+}
+constexpr size_t workspace_bytes(int max_rows, bool pairs) {
+    return ws_counters(max_rows) + ws_partials(max_rows) + ws_cands(max_rows) + kWsFb + ws_pending(max_rows) +
+           (pairs ? ws_pairs(max_rows) : 0);
+}
+
+// The no-alloc entry's rows per call, and the devices it keeps a handle for.
+constexpr int kStaticRows = SPX_NOALLOC_MAX_ROWS;
+constexpr int kMaxDevices = 64;
+
 }  // namespace spx
 
 #include <hip/hip_runtime.h>
@@ -156,6 +178,13 @@ hipError_t launch_pair_prep(int rows, const spx_row_params * first, const spx_ro
 hipError_t launch_pair_pick(int rows, const int32_t * ids, const int32_t * status, const int32_t * token_ids,
                             int32_t sem_lo, int32_t sem_hi, int window, const int32_t * hist, const int32_t * hist_off,
                             int32_t * out_ids, int32_t * out_status, hipStream_t s);
+// spx_api.cpp's pieces of the no-alloc entry (spx_noalloc.hip): the LDS a call of the sizes needs, a handle of static
+// storage over a workspace the caller owns, and the per-call limits of such a handle.
+size_t lds_bound(int max_vocab, int max_hist);
+spx_status report(spx_status s, const char * msg);  // sets spx_last_error()'s message
+spx_status report_hip(hipError_t e, const char * what);
+spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out);
+void set_call_limits(spx_sampler * s, int vocab, int max_hist, int max_out);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);
 hipError_t lds_limit_f32_256(int bytes);
