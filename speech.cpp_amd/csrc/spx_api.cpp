@@ -10,6 +10,7 @@
 
 #include "../../include/spx_sampler.h"
 #include "spx_internal.h"
+#include "spx_plan.h"
 
 struct spx_sampler {
     int device = 0;
@@ -41,85 +42,10 @@ spx_status hip_fail(hipError_t e, const char * what) {
     return fail(SPX_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
 }
 
-size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
-
-// The kernel's LDS layout for one call: the control block, reduction scratch, the chunk's special-token words, its
-// list of history tokens (a power of two of entries, at least max_hist), then the candidate buffer and the sorted
-// candidates (also the radix path's histograms), which the wide path's region overlays.
-size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, bool has_hist, bool has_ban, int max_hist) {
-    using namespace spx;
-    size_t off = 0;
-    a.off_ctl = (int) off;
-    off += kCtlBytes;
-    a.off_red = (int) off;
-    off += 1280;
-    const size_t words = (size_t) (chunk + 31) / 32;
-    a.off_spec = (int) off;
-    if (has_hist || has_ban) off += align_up(words * 4, 16);
-    size_t cap = 1;
-    while (cap < (size_t) max_hist) cap *= 2;
-    a.own_cap = (int) cap;
-    a.off_own = (int) off;
-    if (has_hist) off += cap * 4;
-    a.cand_cap = std::max(2 * block, kSortCap);  // also where the merge of a row's chunks sorts up to kSortCap entries
-    off = align_up(off, 16);
-    a.off_cand = (int) off;
-    a.off_sort = (int) (off + (size_t) a.cand_cap * 8);
-    if (!greedy_only) off = (size_t) a.off_sort + (size_t) kSortCap * 8;
-    a.lds_bytes = (int) off;
-    return off;
-}
-
-// The resolving kernel's launch record from the sampling one: a whole row per work-group (its special tokens over the
-// whole vocabulary), 1024 threads for large vocabularies, and an LDS layout whose last region is the wide path's (the
-// radix path's 2 x kKeep listed entries and its histograms fit there too).
-size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist) {
-    using namespace spx;
-    r = a;
-    r.block = a.vocab >= kBigVocab ? kBlockResolve : kBlockSmall;
-    r.splits = 1;
-    r.chunk = a.vocab;
-    size_t off = 0;
-    r.off_ctl = (int) off;
-    off += kCtlBytes;
-    r.off_red = (int) off;
-    off += 1280;
-    r.off_spec = (int) off;
-    off += align_up((size_t) (a.vocab + 31) / 32 * 4, 16);
-    size_t cap = 1;
-    while (cap < (size_t) max_hist) cap *= 2;
-    r.own_cap = (int) cap;
-    r.off_own = (int) off;
-    off += cap * 4;
-    off = align_up(off, 16);
-    r.off_cand = (int) off;
-    r.off_sort = (int) (off + 2 * kKeep * 8);
-    const size_t wide = r.block == kBlockResolve ? wide_lds_bytes<kBlockResolve>() : wide_lds_bytes<kBlockSmall>();
-    off = std::max((size_t) r.off_sort + 3 * 1024, off + wide);
-    r.lds_bytes = (int) off;
-    return off;
-}
-
 void plan_launch(spx_sampler * s, spx::Launch & a, bool greedy_only, bool has_hist, bool has_ban) {
-    using namespace spx;
-    const int block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
-    // Chunks per row: about one work-group of 1024 threads, or four of 256, per CU; chunks of at least one step of the
-    // work-group, and few enough that the row's last chunk can merge them.
-    const int per_cu = block == kBlockBig ? 1 : 4;
-    const int max_splits = greedy_only ? kMaxSplitsGreedy : kMaxSplits;
-    int splits = std::max(1, (per_cu * s->cus + a.rows - 1) / std::max(a.rows, 1));
-    splits = std::min(splits, max_splits);
-    splits = std::min(splits, std::max(1, a.vocab / (kE * block)));
-    int chunk = (a.vocab + splits - 1) / splits;
-    chunk = (int) align_up((size_t) chunk, 64);
-    splits = (a.vocab + chunk - 1) / chunk;
-    a.block = block;
-    a.splits = splits;
-    a.chunk = chunk;
-    a.nwg = a.rows * splits;
-    plan_lds(a, block, chunk, greedy_only, has_hist, has_ban, s->max_hist);
-    s->last_block = block;
-    s->last_splits = splits;
+    spx::plan_rows(a, s->cus, s->max_hist, greedy_only, has_hist, has_ban);
+    s->last_block = a.block;
+    s->last_splits = a.splits;
 }
 
 spx_status check_common(spx_sampler * s, const void * logits, int dtype, int rows, int vocab, int64_t ld,
@@ -210,7 +136,7 @@ void carve_workspace(spx_sampler * s, void * ws, int max_rows, bool pairs) {
         s->pair_map = (int32_t *) p;
         s->pair_ids = s->pair_map + max_rows;
         s->pair_status = s->pair_ids + max_rows;
-        s->zero_u = (double *) align_up((size_t) (s->pair_status + max_rows), 8);
+        s->zero_u = (double *) spx::align_up((size_t) (s->pair_status + max_rows), 8);
     }
     s->base.row_map = nullptr;
     s->base.hist_stride = 0;
@@ -228,19 +154,6 @@ namespace spx {
 spx_status report(spx_status s, const char * msg) { return fail(s, msg); }
 spx_status report_hip(hipError_t e, const char * what) { return hip_fail(e, what); }
 
-size_t lds_bound(int max_vocab, int max_hist) {
-    // The LDS a call can ask for: the largest history, and a chunk that is the whole vocabulary, in either work-group
-    // size a call may take, and the resolving kernel's.
-    size_t lds_max = 0;
-    for (int block : {kBlockBig, kBlockSmall}) {
-        Launch probe{};
-        lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
-    }
-    Launch probe{}, res{};
-    probe.vocab = max_vocab;
-    return std::max(lds_max, plan_resolve(res, probe, max_hist));
-}
-
 // Handles over the no-alloc entry's workspace: host records of static storage, one per device.
 spx_sampler g_bound[kMaxDevices];
 
@@ -251,7 +164,7 @@ spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out)
     s->max_rows = max_rows;
     int cus = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) == hipSuccess && cus > 0) s->cus = cus;
-    const hipError_t e = set_lds_limits(160 * 1024);
+    const hipError_t e = set_lds_limits((int) spx::kLdsMax);
     if (e != hipSuccess) return hip_fail(e, "hipFuncSetAttribute");
     carve_workspace(s, ws, max_rows, false);
     s->ws = nullptr;  // not the handle's to free
@@ -293,7 +206,7 @@ spx_status spx_sampler_create(spx_sampler ** out, int max_rows, int max_vocab, i
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, s->device) == hipSuccess && cus > 0)
         s->cus = cus;
     const size_t lds_max = spx::lds_bound(max_vocab, max_hist);
-    if (lds_max > 160 * 1024) {
+    if (lds_max > spx::kLdsMax) {
         delete s;
         return fail(SPX_ERR_INVALID_ARGUMENT, "max_vocab and max_hist need more LDS than a CU holds");
     }

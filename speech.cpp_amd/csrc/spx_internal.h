@@ -178,9 +178,8 @@ hipError_t launch_pair_prep(int rows, const spx_row_params * first, const spx_ro
 hipError_t launch_pair_pick(int rows, const int32_t * ids, const int32_t * status, const int32_t * token_ids,
                             int32_t sem_lo, int32_t sem_hi, int window, const int32_t * hist, const int32_t * hist_off,
                             int32_t * out_ids, int32_t * out_status, hipStream_t s);
-// spx_api.cpp's pieces of the no-alloc entry (spx_noalloc.hip): the LDS a call of the sizes needs, a handle of static
-// storage over a workspace the caller owns, and the per-call limits of such a handle.
-size_t lds_bound(int max_vocab, int max_hist);
+// spx_api.cpp's pieces of the no-alloc entry (spx_noalloc.hip): its error messages, a handle of static storage over
+// a workspace the caller owns, and the per-call limits of such a handle.
 spx_status report(spx_status s, const char * msg);  // sets spx_last_error()'s message
 spx_status report_hip(hipError_t e, const char * what);
 spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out);

@@ -9,6 +9,7 @@
 
 #include "../../include/spx_sampler.h"
 #include "spx_internal.h"
+#include "spx_plan.h"
 
 namespace {
 
@@ -42,7 +43,7 @@ extern "C" spx_status spx_sample_rows_noalloc(const void * d_logits, int dtype, 
     if (rows < 0 || rows > spx::kStaticRows) return spx::report(SPX_ERR_INVALID_ARGUMENT, "rows outside [0, SPX_NOALLOC_MAX_ROWS]");
     if (vocab <= 0 || max_hist < 0 || max_out < 0 || max_out > spx::kKeep) return spx::report(SPX_ERR_INVALID_ARGUMENT, "vocab, max_hist or max_out out of range");
     if (d_out_cand_ids && max_out == 0) return spx::report(SPX_ERR_INVALID_ARGUMENT, "candidate outputs with max_out 0");
-    if (spx::lds_bound(vocab, max_hist) > 160 * 1024) return spx::report(SPX_ERR_INVALID_ARGUMENT, "vocab and max_hist need more LDS than a CU holds");
+    if (spx::lds_bound(vocab, max_hist) > spx::kLdsMax) return spx::report(SPX_ERR_INVALID_ARGUMENT, "vocab and max_hist need more LDS than a CU holds");
     int device = 0;
     hipError_t e = hipGetDevice(&device);
     if (e != hipSuccess) return spx::report_hip(e, "hipGetDevice");
