@@ -7,19 +7,27 @@
  * std::partial_sort with the same comparator, the same top-p rule) and cites it. Paths are relative to the reference
  * checkout (nyosegawa/speech.cpp 0.11.1).
  *
- * Parity pins (see tests/test_oracle_*.py):
+ * Parity pins (tests/test_oracle_ref.py, test_golden.py, test_oracle_semantics.py, test_oracle_families.py,
+ * test_host_layer.py):
  *   orc_uniform_fill, orc_pick        bit-exact against the reference's own src/common/sampling.cpp, compiled
- *                                     unchanged into oracle/_ref, and the known answers of
- *                                     checks/qwen3-tts/qwen3-tts-sampler-check.cpp:98-115
- *   orc_tf_candidates / orc_tf_sample transformers' logits processors (installed transformers, the library the
- *                                     reference restates) on golden fixtures; the refusals of
- *                                     qwen3-tts-sampler-check.cpp:70-91 and qwen3-tts-graph-sampler-check.cpp:162-186;
- *                                     closed forms (greedy = first max, top-k 1 = argmax, top-p 1 and top-k 0 = full
- *                                     softmax) and brute force on tiny vocabularies
- *   orc_haru_candidates               a torch restatement of sample_token() on golden fixtures within the tolerance of
- *                                     checks/haru/haru-sampling-check.cpp:36; ties to the lower id; closed forms
- *   orc_fish_candidates               a torch restatement of sample_top_k_top_p() on golden fixtures within the
- *                                     tolerances of checks/drama3/drama3-sampler-check.cpp:36-41; closed forms
+ *                                     unchanged into oracle/_ref (and the fixtures tests/golden/reference_sampling.npz
+ *                                     it wrote), and the known answers of checks/qwen3-tts/qwen3-tts-sampler-check.cpp
+ *                                     :98-115
+ *   orc_tf_candidates / orc_tf_sample the refusals of qwen3-tts-sampler-check.cpp:70-91 and
+ *                                     qwen3-tts-graph-sampler-check.cpp:162-186; closed forms: greedy = the first
+ *                                     maximum, top-k 1 = argmax, top-k 0 and top-p 1 = the full softmax, top-p after
+ *                                     top-k normalized over the k kept and not again after the cut, the crossing
+ *                                     token kept (>=), the repetition penalty's sign rule over a deduplicated history;
+ *                                     brute-force draw frequencies on tiny vocabularies
+ *   orc_haru_candidates               ties to the lower id; every token listed with the zeroed ones; the float32
+ *                                     running sum of the top-p rule (rows where a double sum decides otherwise);
+ *                                     greedy at temperature <= 0; brute force
+ *   orc_fish_candidates               the temperature floor of 1e-5; shares over the softmax of every logit; the token
+ *                                     passing top_p dropped, the first always kept; ties to the lower id; brute force
+ *   orc_talker_bans, orc_drama3_main  transformers' SuppressTokens / MinNewTokensLength definitions; the redraw rules
+ *                                     of checks/drama3/drama3-sampler-check.cpp:121-142
+ *   the refusal messages              the reference's temperature_overflow() from oracle/_ref, for several
+ *                                     temperatures (shortest round-trip floats)
  *   presence / frequency penalty      parity unpinned against any reference (the reference has none); pinned by its
  *                                     closed form l - frequency*count - presence
  */

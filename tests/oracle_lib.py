@@ -160,3 +160,33 @@ def drama3_main(logits, first, again, u_first, u_again, token_ids, semantic_begi
     st = oracle().orc_drama3_main(_ptr(l), len(l), _ptr(f), _ptr(g), u_first, u_again, _ptr(t), semantic_begin,
                                   semantic_end, window, _ptr(h), len(h), _ptr(out))
     return st, int(out[0])
+
+
+def haru_zeroing(p32, top_p, double_sum=False):
+    """Which of Haru's probabilities (float32, in the row's order) the top-p rule zeroes: !(cumulative - p < top_p),
+    with the running sum in float32 as src/families/haru/sampler.cpp:54-58 keeps it, or (double_sum) in double."""
+    p32 = np.asarray(p32, dtype=np.float32)
+    if double_sum:
+        before = np.concatenate([[0.0], np.cumsum(p32.astype(np.float64))[:-1]])
+        return ~(before < float(np.float32(top_p)))
+    cum = np.add.accumulate(p32, dtype=np.float32)  # sequential, in order
+    return ~((cum - p32) < np.float32(top_p))
+
+
+def haru_float_flip(logits, temperature):
+    """A top_p (float32, below 1) at which Haru's float32 running sum zeroes a different set of tokens than a double
+    sum would, for a row drawing over every token, or None. Reads the probabilities from the oracle at top_p 1."""
+    st, _, p = haru_candidates(logits, temperature, 0, 1.0)
+    if st != 0:
+        return None
+    p32 = p.astype(np.float32)
+    cum = np.add.accumulate(p32, dtype=np.float32)
+    before_f = cum - p32
+    before_d = np.concatenate([[0.0], np.cumsum(p32.astype(np.float64))[:-1]])
+    # a token whose float32 share before it lies above the double one: top_p = that float32 value zeroes it in float32
+    # (not below itself) and keeps it in double
+    for i in np.nonzero(before_f.astype(np.float64) > before_d)[0]:
+        t = np.float32(before_f[i])
+        if 0 < t < 1 and not np.array_equal(haru_zeroing(p32, t), haru_zeroing(p32, t, True)):
+            return float(t)
+    return None

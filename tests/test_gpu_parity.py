@@ -314,6 +314,66 @@ def test_draws_over_one_row(sampler, name):
     assert dev.max() <= 5.0, (int(np.argmax(dev)), dev.max())
 
 
+@pytest.mark.parametrize("vocab", [512, 8192, 151936])
+def test_haru_float32_running_sum_on_the_device(sampler, vocab):
+    # Rows whose float32 running sum and a double sum put a token on different sides of top_p
+    # (src/families/haru/sampler.cpp:54-58): the whole candidate list, zeros included, must be the oracle's, and u
+    # aimed inside the flipped token's share must pick it or not as the float32 rule says.
+    import torch
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(vocab)
+    rows, ts = [], []
+    while len(rows) < 3:
+        l = rng.normal(0, 1.5, vocab).astype(np.float32)
+        t = oracle_lib.haru_float_flip(l, 1.0)
+        if t is not None:
+            rows.append(l)
+            ts.append(t)
+    logits = np.stack(rows)
+    p = spx.row_params(3, spx.HARU, temperature=1.0, top_k=0, top_p=np.array(ts, dtype=np.float32))
+    d_logits, d_params = torch.from_numpy(logits).cuda(), spx.device_params(p)
+    toks, wts, n, status = sampler.candidates_rows(d_logits, d_params, vocab)
+    torch.cuda.synchronize()
+    toks, wts, n, status = toks.cpu().numpy(), wts.cpu().numpy(), n.cpu().numpy(), status.cpu().numpy()
+    us = []
+    for r in range(3):
+        st, otok, ow = oracle_lib.haru_candidates(logits[r], 1.0, 0, ts[r])
+        assert status[r] == st == 0 and n[r] == len(otok) == vocab
+        np.testing.assert_array_equal(toks[r], otok)
+        np.testing.assert_array_equal(wts[r] == 0, ow == 0)
+        np.testing.assert_allclose(wts[r], ow, rtol=1e-6, atol=0)
+        # u in the middle of the share the double sum would give the first token the two sums treat differently
+        _, _, p1 = oracle_lib.haru_candidates(logits[r], 1.0, 0, 1.0)
+        i = int(np.argmax(oracle_lib.haru_zeroing(p1, ts[r]) != oracle_lib.haru_zeroing(p1, ts[r], True)))
+        wd = np.where(oracle_lib.haru_zeroing(p1, ts[r], True), 0.0, p1)
+        c = np.cumsum(wd) / wd.sum()
+        lo = c[i - 1] if i > 0 else 0.0
+        us.append(lo + (c[i] - lo) / 2)
+    w = workloads.Workload(name="haru float32 sum", logits=logits, dtype="f32", params=p, u=np.array(us), hist=None,
+                           hist_off=None, banned=None, banned_stride=0)
+    reports, _, _ = oracle_lib.sample_rows(w)
+    gpu = gpu_harness.run_gpu(sampler, w)
+    for r in range(3):  # no excuse: the decision at top_p is the point of the row
+        assert reports[r]["boundary"] > 1e-12, r
+        assert (gpu["status"][r], gpu["ids"][r], gpu["kept"][r]) == (0, reports[r]["id"], reports[r]["kept"]), r
+
+
+def test_transformers_top_p_over_the_top_k_and_fish_floor_on_the_device(sampler):
+    # The closed forms the oracle is pinned by, on the device: top-k 2 then top-p 0.55 over weights 0.4, 0.3, 0.2, 0.1
+    # keeps one token (normalized over the two kept); Drama 3's temperature floor of 1e-5.
+    spx = workloads.spx_module()
+    tf_l = np.log(np.array([0.4, 0.3, 0.2, 0.1] * 1)).astype(np.float32)
+    for u in (0.0, 0.5, 0.99):
+        w = _one(dict(temperature=1.0, top_k=2, top_p=0.55), tf_l, u=u)
+        _, gpu, reps = check(sampler, w, allow_explained=False)
+        assert gpu["ids"][0] == 0 and gpu["kept"][0] == 1
+    fish_l = np.array([0.0, -1e-5, -3e-5], dtype=np.float32)
+    for t in (1e-7, 0.0):
+        for u in (0.2, 0.8, 0.99):
+            w = _one(dict(flavor=spx.FISH, temperature=t, top_k=3, top_p=1.0), fish_l, u=u)
+            check(sampler, w, allow_explained=False)
+
+
 def test_long_histories(sampler):
     # Histories of 8192 ids (the talker's grows one id per frame without a bound), with repetition, presence and
     # frequency penalties, on both work-group sizes.

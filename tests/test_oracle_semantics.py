@@ -173,3 +173,52 @@ def test_brute_force_draw_frequencies(flavor, k, p):
     share = w / w.sum()
     for t, s in zip(tok.tolist(), share.tolist()):
         assert abs(counts.get(t, 0) / len(grid) - s) < 2.0 / len(grid) + 1e-12
+
+
+def test_transformers_top_p_after_top_k_is_over_the_k_kept():
+    # qwen3-tts/sampler.cpp:84-99: the weights are normalized over the top k before the top-p rule reads them, and
+    # are not normalized again after it. Weights 0.4, 0.3, 0.2, 0.1 with k = 2 are 4/7 and 3/7 over the two kept, so
+    # top_p 0.55 keeps one token (4/7 >= 0.55), where shares over the whole vocabulary (0.4 < 0.55) would keep two.
+    l = np.log(np.array([0.4, 0.3, 0.2, 0.1])).astype(np.float32)
+    st, tok, w = oracle_lib.tf_candidates(l, tf(top_k=2, top_p=0.55))
+    assert st == 0 and list(tok) == [0] and abs(w[0] - 4 / 7) < 1e-6
+    st, tok, w = oracle_lib.tf_candidates(l, tf(top_k=0, top_p=0.55))
+    assert list(tok) == [0, 1] and np.allclose(w, [0.4, 0.3], rtol=1e-6)
+    st, tok, w = oracle_lib.tf_candidates(l, tf(top_k=3, top_p=0.99))
+    assert list(tok) == [0, 1, 2] and np.allclose(w, [4 / 9, 3 / 9, 2 / 9], rtol=1e-6)
+    # top_p just above 4/7 + 3/7 - 1e-6: both kept, weights still over k
+    st, tok, w = oracle_lib.tf_candidates(l, tf(top_k=2, top_p=0.6))
+    assert list(tok) == [0, 1] and np.allclose(w, [4 / 7, 3 / 7], rtol=1e-6)
+
+
+def test_fish_temperature_floor():
+    # drama3/sampler.cpp:31: t = max(temperature, 1e-5). At or below the floor the logits are divided by 1e-5, so
+    # logits 0, -1e-5, -3e-5 weigh exp(0), exp(-1), exp(-3) (the weights are the unnormalized exponentials).
+    l = np.array([0.0, -1e-5, -3e-5], dtype=np.float32)
+    want = np.exp(np.array([0.0, -1.0, -3.0]))
+    for t in (1e-5, 1e-7, 0.0, -2.0):
+        st, tok, w = oracle_lib.fish_candidates(l, t, 3, 2.0)
+        assert st == 0 and list(tok) == [0, 1, 2]
+        assert np.allclose(w, want, rtol=1e-6), (t, w)
+    st, tok, w = oracle_lib.fish_candidates(l, 2e-5, 3, 2.0)  # above the floor: half the spread
+    assert np.allclose(w, np.exp(np.array([0.0, -0.5, -1.5])), rtol=1e-6)
+
+
+def test_haru_top_p_reads_a_float32_running_sum():
+    # haru/sampler.cpp:54-58: the top-p rule compares a float32 running sum less the token's own float32 probability
+    # with top_p. Rows whose float32 and double sums put a token on different sides of top_p must follow float32.
+    rng = np.random.default_rng(8)
+    found = 0
+    for _ in range(50):
+        l = rng.normal(0, 1.5, 512).astype(np.float32)
+        t = oracle_lib.haru_float_flip(l, 1.0)
+        if t is None:
+            continue
+        _, _, p = oracle_lib.haru_candidates(l, 1.0, 0, 1.0)
+        st, tok, w = oracle_lib.haru_candidates(l, 1.0, 0, t)
+        assert st == 0 and len(tok) == 512
+        zeroed = w == 0
+        assert np.array_equal(zeroed, oracle_lib.haru_zeroing(p, t))
+        assert not np.array_equal(zeroed, oracle_lib.haru_zeroing(p, t, double_sum=True))
+        found += 1
+    assert found >= 5
