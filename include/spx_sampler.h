@@ -205,6 +205,45 @@ typedef struct spx_stats {
 } spx_stats;
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out);
 
+/*
+ * Haru's DRY repetition penalty (src/families/haru/sampler.h:35-38, DryConfig): the settings the model file holds.
+ */
+typedef struct spx_dry_config {
+    double multiplier, base, max_penalty;
+    int32_t allowed_length, lookback, max_match_length, reserved;
+} spx_dry_config;
+
+/* Tokens a DRY state may hold (lookback + max_match_length + 1) and exempt ids a call takes. */
+#define SPX_DRY_MAX_HISTORY 4096
+#define SPX_DRY_MAX_EXEMPT 8
+
+/*
+ * Dry::update (src/families/haru/sampler.cpp:87-110) for many text streams at once, their states on the device: row r
+ * appends d_tokens[r] to its history d_hist[r * hist_stride ...] of d_len[r] tokens unless the token is one of the
+ * n_exempt ids (or negative: a row whose draw failed), keeping the last lookback + max_match_length + 1 tokens.
+ * hist_stride must hold that many (at most SPX_DRY_MAX_HISTORY). The penalties follow from the history when
+ * spx_haru_shape_rows reads it, as Dry::update computes them.
+ */
+spx_status spx_dry_update_rows(int rows, const spx_dry_config * config, const int32_t * exempt, int n_exempt,
+                               const int32_t * d_tokens, int32_t * d_hist, int32_t * d_len, int hist_stride,
+                               void * stream);
+
+/*
+ * haru::shape_logits (src/families/haru/sampler.cpp:116-124) for many rows of fp32 text logits, in place: each row's
+ * DRY penalties (Dry::update's, from its history: for every token that would extend a sequence of at least
+ * allowed_length that occurred within the last lookback tokens, min(max_penalty, multiplier *
+ * base^(length - allowed_length)) of its longest one, in double) subtracted as floats (Dry::apply, :112-114); the
+ * logits of pad and eop replaced by d_silent[2r] and d_silent[2r + 1]; eop_bias added to eop's where it is not 0;
+ * and, where d_must_speak[r] is nonzero, pad, eop and eos set to -inf (d_must_speak may be null). History ids
+ * outside [0, vocab) are never written. The optional outputs list each row's penalties as Dry::penalties() does, by
+ * rising token: d_out_pen_tokens and d_out_pen of rows x pen_cap, d_out_npen their count (may exceed pen_cap).
+ */
+spx_status spx_haru_shape_rows(float * d_logits, int rows, int vocab, int64_t ld, const spx_dry_config * config,
+                               const int32_t * exempt, int n_exempt, const int32_t * d_hist, const int32_t * d_len,
+                               int hist_stride, const float * d_silent, int32_t pad, int32_t eop, int32_t eos,
+                               float eop_bias, const uint8_t * d_must_speak, int32_t * d_out_pen_tokens,
+                               double * d_out_pen, int32_t * d_out_npen, int pen_cap, void * stream);
+
 /* Rows per call of spx_sample_rows_noalloc. */
 #define SPX_NOALLOC_MAX_ROWS 2048
 

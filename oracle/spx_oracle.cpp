@@ -12,6 +12,7 @@
 #include <numeric>
 #include <random>
 #include <thread>
+#include <map>
 #include <vector>
 
 namespace {
@@ -479,3 +480,63 @@ int orc_final_logits(const float * logits, int vocab, const spx_row_params * p, 
 }
 
 }  // extern "C"
+
+// ---- Haru's DRY and shape_logits ----
+
+// Dry (src/families/haru/sampler.cpp:83-114) run over `tokens` from a fresh state: the history it keeps and the
+// penalties of its last update, by rising token (std::map order), as doubles.
+int orc_dry_run(const spx_dry_config * c, const int32_t * exempt, int n_exempt, const int32_t * tokens, int n_tokens,
+                int32_t * hist_out, int * n_hist, int32_t * pen_tokens, double * pen, int cap) {
+    auto is_exempt = [&](int32_t t) {
+        for (int i = 0; i < n_exempt; i++)
+            if (exempt[i] == t) return true;
+        return false;
+    };
+    std::vector<int32_t> h;
+    std::vector<std::pair<int32_t, double>> out;
+    const size_t size = (size_t) c->lookback + (size_t) c->max_match_length + 1;
+    for (int s = 0; s < n_tokens; s++) {
+        const int32_t token = tokens[s];
+        if (is_exempt(token)) continue;  // the state and its penalties stay
+        h.push_back(token);
+        if (h.size() > size) h.erase(h.begin(), h.begin() + (std::ptrdiff_t) (h.size() - size));
+        out.clear();
+        const int64_t n = (int64_t) h.size();
+        if (n < std::max(1, c->allowed_length)) continue;
+        std::map<int32_t, int> best;  // token -> its longest match
+        const int32_t last = h[(size_t) (n - 1)];
+        const int64_t stop = std::max<int64_t>(0, n - 1 - c->lookback);
+        for (int64_t j = n - 2; j >= stop; j--) {
+            if (h[(size_t) j] != last) continue;
+            int len = 1;
+            while (len < c->max_match_length && j - len >= 0 && h[(size_t) (j - len)] == h[(size_t) (n - 1 - len)]) len++;
+            if (len < c->allowed_length) continue;
+            const int32_t next = h[(size_t) (j + 1)];
+            auto it = best.find(next);
+            if (it == best.end()) best.emplace(next, len);
+            else if (len > it->second) it->second = len;
+        }
+        for (const auto & kv : best) {
+            if (is_exempt(kv.first)) continue;
+            out.emplace_back(kv.first, std::min(c->max_penalty,
+                                                c->multiplier * std::pow(c->base, kv.second - c->allowed_length)));
+        }
+    }
+    if (hist_out) std::copy(h.begin(), h.end(), hist_out);
+    if (n_hist) *n_hist = (int) h.size();
+    for (size_t i = 0; i < out.size() && (int) i < cap; i++) {
+        pen_tokens[i] = out[i].first;
+        pen[i] = out[i].second;
+    }
+    return (int) out.size();
+}
+
+// shape_logits (src/families/haru/sampler.cpp:112-124) with the penalties of orc_dry_run.
+void orc_haru_shape(float * logits, const int32_t * pen_tokens, const double * pen, int n_pen, const float * silent,
+                    int32_t pad, int32_t eop, int32_t eos, float eop_bias, int must_speak) {
+    for (int i = 0; i < n_pen; i++) logits[pen_tokens[i]] -= (float) pen[i];
+    logits[pad] = silent[0];
+    logits[eop] = silent[1];
+    if (eop_bias != 0.0f) logits[eop] += eop_bias;
+    if (must_speak) logits[pad] = logits[eop] = logits[eos] = -INFINITY;
+}

@@ -28,6 +28,10 @@
  *                                     of checks/drama3/drama3-sampler-check.cpp:121-142
  *   the refusal messages              the reference's temperature_overflow() from oracle/_ref, for several
  *                                     temperatures (shortest round-trip floats)
+ *   orc_dry_run, orc_haru_shape       hand-derived known answers of Dry::update (matches, the longest per token, the
+ *                                     lookback and max_match_length limits, exempt ids, the window's trimming) and
+ *                                     shape_logits (the order of its edits); the reference's DRY fixtures
+ *                                     (dry.jsonl of checks/haru/haru-sampling-check.cpp) are not in the checkout
  *   presence / frequency penalty      parity unpinned against any reference (the reference has none); pinned by its
  *                                     closed form l - frequency*count - presence
  */
@@ -99,6 +103,18 @@ void orc_talker_bans(int vocab, int suppressed_tokens, int32_t end_of_speech, in
 int orc_drama3_main(const float * logits, int vocab, const spx_row_params * first, const spx_row_params * again,
                     double u_first, double u_again, const int32_t * token_ids, int32_t semantic_begin,
                     int32_t semantic_end, int window, const int32_t * history, int n_history, int32_t * out_id);
+
+/*
+ * Haru's Dry (src/families/haru/sampler.cpp:83-114) run over n_tokens tokens from a fresh state: writes the history it
+ * keeps (hist_out, *n_hist) and the penalties of its last update by rising token (the first `cap`); returns their
+ * count.
+ */
+int orc_dry_run(const spx_dry_config * c, const int32_t * exempt, int n_exempt, const int32_t * tokens, int n_tokens,
+                int32_t * hist_out, int * n_hist, int32_t * pen_tokens, double * pen, int cap);
+
+/* haru::shape_logits (src/families/haru/sampler.cpp:116-124) of one row in place, with orc_dry_run's penalties. */
+void orc_haru_shape(float * logits, const int32_t * pen_tokens, const double * pen, int n_pen, const float * silent,
+                    int32_t pad, int32_t eop, int32_t eos, float eop_bias, int must_speak);
 
 #ifdef __cplusplus
 }

@@ -32,7 +32,15 @@ assert ROW_PARAMS.itemsize == 32
 # Every symbol include/spx_sampler.h declares.
 EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_candidates_rows",
            "spx_sample_chain",
-           "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats", "spx_sample_rows_noalloc"]
+           "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats", "spx_sample_rows_noalloc",
+           "spx_dry_update_rows", "spx_haru_shape_rows"]
+
+
+class DryConfig(ctypes.Structure):
+    """spx_dry_config: Haru's DRY settings (src/families/haru/sampler.h:35-38)."""
+    _fields_ = [("multiplier", ctypes.c_double), ("base", ctypes.c_double), ("max_penalty", ctypes.c_double),
+                ("allowed_length", ctypes.c_int32), ("lookback", ctypes.c_int32), ("max_match_length", ctypes.c_int32),
+                ("reserved", ctypes.c_int32)]
 
 
 class SpxStats(ctypes.Structure):
@@ -78,6 +86,11 @@ def load_library(path=LIB_PATH):
     lib.spx_sample_rows_noalloc.argtypes = [vp, i32, i32, i32, i64, vp, vp, i32, vp, i64, vp, vp, vp, vp, vp, vp, vp,
                                             i32, vp]
     lib.spx_sample_rows_noalloc.restype = i32
+    lib.spx_dry_update_rows.argtypes = [i32, ctypes.POINTER(DryConfig), vp, i32, vp, vp, vp, i32, vp]
+    lib.spx_dry_update_rows.restype = i32
+    lib.spx_haru_shape_rows.argtypes = [vp, i32, i32, i64, ctypes.POINTER(DryConfig), vp, i32, vp, vp, i32, vp, i32,
+                                        i32, i32, ctypes.c_float, vp, vp, vp, vp, i32, vp]
+    lib.spx_haru_shape_rows.restype = i32
     _lib = lib
     return lib
 
@@ -259,3 +272,49 @@ def pack_bans(banned_ids_per_row, vocab):
         ids = ids[(ids >= 0) & (ids < vocab)]
         np.bitwise_or.at(out[r], ids >> 5, (np.uint32(1) << (ids & 31).astype(np.uint32)))
     return out
+
+
+class DryStates:
+    """The DRY states of `rows` text streams on the device (Haru's Dry per stream): histories of `hist_stride` ids and
+    their lengths, the config and the exempt ids (pad, eop, eos in the reference)."""
+
+    def __init__(self, rows, config, exempt, hist_stride=None, device="cuda"):
+        import torch
+        self.lib = load_library()
+        self.config = config
+        self.exempt = np.ascontiguousarray(exempt, dtype=np.int32)
+        self.stride = hist_stride or (config.lookback + config.max_match_length + 1)
+        self.rows = rows
+        self.hist = torch.zeros((rows, self.stride), dtype=torch.int32, device=device)
+        self.len = torch.zeros(rows, dtype=torch.int32, device=device)
+
+    def _check(self, status):
+        if status != 0:
+            raise SamplerError(f"spx status {status}: {self.lib.spx_last_error().decode()}")
+
+    def update(self, tokens, stream=None):
+        """Dry::update of every stream with its drawn token (an int32 device tensor of rows)."""
+        import torch
+        s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        self._check(self.lib.spx_dry_update_rows(self.rows, ctypes.byref(self.config),
+                                                 self.exempt.ctypes.data_as(ctypes.c_void_p), len(self.exempt),
+                                                 _ptr(tokens), _ptr(self.hist), _ptr(self.len), self.stride,
+                                                 ctypes.c_void_p(s)))
+
+    def shape(self, logits, silent, pad, eop, eos, eop_bias=0.0, must_speak=None, pen_cap=0, stream=None):
+        """shape_logits of every row of `logits` (rows x vocab float32, in place) with its stream's penalties; returns
+        (penalty tokens, penalties, counts) when pen_cap > 0."""
+        import torch
+        rows, vocab = logits.shape
+        s = stream if stream is not None else torch.cuda.current_stream().cuda_stream
+        toks = pens = n = None
+        if pen_cap:
+            toks = torch.full((rows, pen_cap), -1, dtype=torch.int32, device=logits.device)
+            pens = torch.zeros((rows, pen_cap), dtype=torch.float64, device=logits.device)
+            n = torch.zeros(rows, dtype=torch.int32, device=logits.device)
+        self._check(self.lib.spx_haru_shape_rows(
+            _ptr(logits), rows, vocab, logits.stride(0), ctypes.byref(self.config),
+            self.exempt.ctypes.data_as(ctypes.c_void_p), len(self.exempt), _ptr(self.hist), _ptr(self.len),
+            self.stride, _ptr(silent), pad, eop, eos, eop_bias, _ptr(must_speak), _ptr(toks), _ptr(pens), _ptr(n),
+            pen_cap, ctypes.c_void_p(s)))
+        return toks, pens, n

@@ -4,6 +4,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -177,6 +178,39 @@ void set_call_limits(spx_sampler * s, int vocab, int max_hist, int max_out) {
     s->max_hist = max_hist;
     s->max_out = max_out;
     s->base.max_hist = max_hist;
+}
+
+// The DRY settings a call runs with: checked, and the penalty of every match length computed on the host (std::pow,
+// as Dry::update computes it).
+spx_status dry_args(DryArgs & d, const spx_dry_config * c, const int32_t * exempt, int n_exempt, int hist_stride) {
+    if (!c) return fail(SPX_ERR_INVALID_ARGUMENT, "null DRY config");
+    if (n_exempt < 0 || n_exempt > SPX_DRY_MAX_EXEMPT || (n_exempt > 0 && !exempt))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "exempt ids: null, or more than SPX_DRY_MAX_EXEMPT");
+    if (c->lookback < 0 || c->max_match_length < 0) return fail(SPX_ERR_INVALID_ARGUMENT, "negative lookback or max_match_length");
+    const int64_t size = (int64_t) c->lookback + c->max_match_length + 1;
+    if (size > hist_stride || hist_stride > SPX_DRY_MAX_HISTORY)
+        return fail(SPX_ERR_INVALID_ARGUMENT, "hist_stride below lookback + max_match_length + 1, or above SPX_DRY_MAX_HISTORY");
+    d = DryArgs{};
+    d.hist_stride = hist_stride;
+    d.allowed = c->allowed_length;
+    d.lookback = c->lookback;
+    d.max_match = c->max_match_length;
+    d.size = (int) size;
+    d.n_exempt = n_exempt;
+    for (int i = 0; i < n_exempt; i++) d.exempt[i] = exempt[i];
+    // a match is 1 .. max(1, max_match_length) long; its penalty's exponent e = length - allowed_length
+    const int64_t emax = (int64_t) std::max(1, c->max_match_length) - c->allowed_length;
+    const int n = (int) std::max<int64_t>(0, std::min<int64_t>(emax + 1, kDryTable));
+    for (int e = 0; e < n; e++) d.table[e] = std::min(c->max_penalty, c->multiplier * std::pow(c->base, (double) e));
+    d.n_table = n;
+    d.sat = c->max_penalty;
+    if (emax >= kDryTable) {
+        // every longer match takes max_penalty only where the penalties rise with the length and have reached it
+        const bool rising = c->base >= 1.0 && c->multiplier >= 0.0;
+        if (!rising || d.table[kDryTable - 1] != c->max_penalty)
+            return fail(SPX_ERR_INVALID_ARGUMENT, "DRY penalties that do not reach max_penalty within 128 lengths");
+    }
+    return SPX_OK;
 }
 
 }  // namespace spx
@@ -406,6 +440,57 @@ spx_status spx_drama3_main(spx_sampler * s, const void * d_logits, int dtype, in
     e = spx::launch_pair_pick(rows, s->pair_ids, s->pair_status, d_token_ids, semantic_begin, semantic_end, window,
                               d_hist, d_hist_off, d_out_ids, d_out_status, (hipStream_t) stream);
     return e == hipSuccess ? SPX_OK : hip_fail(e, "pair_pick launch");
+}
+
+spx_status spx_dry_update_rows(int rows, const spx_dry_config * config, const int32_t * exempt, int n_exempt,
+                               const int32_t * d_tokens, int32_t * d_hist, int32_t * d_len, int hist_stride,
+                               void * stream) {
+    spx::DryArgs d;
+    const spx_status st = spx::dry_args(d, config, exempt, n_exempt, hist_stride);
+    if (st != SPX_OK) return st;
+    if (rows < 0) return fail(SPX_ERR_INVALID_ARGUMENT, "negative rows");
+    if (rows > 0 && (!d_tokens || !d_hist || !d_len)) return fail(SPX_ERR_INVALID_ARGUMENT, "null tokens, hist or len");
+    d.rows = rows;
+    d.tokens = d_tokens;
+    d.hist_w = d_hist;
+    d.len_w = d_len;
+    const hipError_t e = spx::launch_dry_update(d, (hipStream_t) stream);
+    return e == hipSuccess ? SPX_OK : hip_fail(e, "dry_update launch");
+}
+
+spx_status spx_haru_shape_rows(float * d_logits, int rows, int vocab, int64_t ld, const spx_dry_config * config,
+                               const int32_t * exempt, int n_exempt, const int32_t * d_hist, const int32_t * d_len,
+                               int hist_stride, const float * d_silent, int32_t pad, int32_t eop, int32_t eos,
+                               float eop_bias, const uint8_t * d_must_speak, int32_t * d_out_pen_tokens,
+                               double * d_out_pen, int32_t * d_out_npen, int pen_cap, void * stream) {
+    spx::DryArgs d;
+    const spx_status st = spx::dry_args(d, config, exempt, n_exempt, hist_stride);
+    if (st != SPX_OK) return st;
+    if (rows < 0 || vocab <= 0 || ld < vocab) return fail(SPX_ERR_INVALID_ARGUMENT, "rows, vocab or ld out of range");
+    if (rows > 0 && (!d_logits || !d_hist || !d_len || !d_silent))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "null logits, hist, len or silent logits");
+    if (pad < 0 || pad >= vocab || eop < 0 || eop >= vocab || eos < 0 || eos >= vocab)
+        return fail(SPX_ERR_INVALID_ARGUMENT, "pad, eop or eos outside the vocabulary");
+    if ((d_out_pen_tokens == nullptr) != (d_out_pen == nullptr) || (d_out_pen_tokens && pen_cap <= 0))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "penalty outputs: tokens and penalties go together, with pen_cap > 0");
+    d.logits = d_logits;
+    d.ld = ld;
+    d.rows = rows;
+    d.vocab = vocab;
+    d.hist = d_hist;
+    d.len = d_len;
+    d.silent = d_silent;
+    d.pad = pad;
+    d.eop = eop;
+    d.eos = eos;
+    d.eop_bias = eop_bias;
+    d.must_speak = d_must_speak;
+    d.out_pen_tokens = d_out_pen_tokens;
+    d.out_pen = d_out_pen;
+    d.out_npen = d_out_npen;
+    d.pen_cap = pen_cap;
+    const hipError_t e = spx::launch_haru_shape(d, (hipStream_t) stream);
+    return e == hipSuccess ? SPX_OK : hip_fail(e, "haru_shape launch");
 }
 
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {

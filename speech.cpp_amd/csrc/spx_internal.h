@@ -178,12 +178,43 @@ hipError_t launch_pair_prep(int rows, const spx_row_params * first, const spx_ro
 hipError_t launch_pair_pick(int rows, const int32_t * ids, const int32_t * status, const int32_t * token_ids,
                             int32_t sem_lo, int32_t sem_hi, int window, const int32_t * hist, const int32_t * hist_off,
                             int32_t * out_ids, int32_t * out_status, hipStream_t s);
+// Haru's DRY: the penalty of a match `length - allowed_length` = e past the allowed length is table[e] for
+// e < n_table and `sat` beyond (the table holds every e up to max_match_length - allowed_length, or ends where it has
+// reached max_penalty with base >= 1, after which every penalty is max_penalty). The host computes the table with its
+// std::pow, the function Dry::update calls, so the device's penalties are the reference's bit for bit.
+constexpr int kDryTable = 128;
+struct DryArgs {
+    float * logits;
+    int64_t ld;
+    int rows, vocab;
+    const int32_t * hist;
+    const int32_t * len;
+    int hist_stride, allowed, lookback, max_match, size, n_table, n_exempt;
+    int32_t exempt[SPX_DRY_MAX_EXEMPT];
+    const int32_t * tokens;  // the update's drawn tokens
+    int32_t * hist_w;        // the update's histories and lengths
+    int32_t * len_w;
+    const float * silent;
+    int32_t pad, eop, eos;
+    float eop_bias;
+    const uint8_t * must_speak;
+    int32_t * out_pen_tokens;
+    double * out_pen;
+    int32_t * out_npen;
+    int pen_cap;
+    double sat;
+    double table[kDryTable];
+};
+
 // spx_api.cpp's pieces of the no-alloc entry (spx_noalloc.hip): its error messages, a handle of static storage over
 // a workspace the caller owns, and the per-call limits of such a handle.
 spx_status report(spx_status s, const char * msg);  // sets spx_last_error()'s message
 spx_status report_hip(hipError_t e, const char * what);
 spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out);
 void set_call_limits(spx_sampler * s, int vocab, int max_hist, int max_out);
+spx_status dry_args(DryArgs & d, const spx_dry_config * c, const int32_t * exempt, int n_exempt, int hist_stride);
+hipError_t launch_dry_update(const DryArgs & d, hipStream_t s);
+hipError_t launch_haru_shape(const DryArgs & d, hipStream_t s);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);
 hipError_t lds_limit_f32_256(int bytes);

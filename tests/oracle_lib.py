@@ -53,6 +53,10 @@ def oracle():
         lib.orc_drama3_main.argtypes = [vp, i32, vp, vp, ctypes.c_double, ctypes.c_double, vp, i32, i32, i32, vp, i32,
                                         vp]
         lib.orc_drama3_main.restype = i32
+        lib.orc_dry_run.argtypes = [vp, vp, i32, vp, i32, vp, vp, vp, vp, i32]
+        lib.orc_dry_run.restype = i32
+        lib.orc_haru_shape.argtypes = [vp, vp, vp, i32, vp, i32, i32, i32, ctypes.c_float, i32]
+        lib.orc_haru_shape.restype = None
         _oracle = lib
     return _oracle
 
@@ -190,3 +194,27 @@ def haru_float_flip(logits, temperature):
         if 0 < t < 1 and not np.array_equal(haru_zeroing(p32, t), haru_zeroing(p32, t, True)):
             return float(t)
     return None
+
+
+def dry_run(config, exempt, tokens):
+    """Haru's Dry over `tokens` from a fresh state: (history kept, penalty tokens, penalties)."""
+    ex = np.ascontiguousarray(exempt, dtype=np.int32)
+    t = np.ascontiguousarray(tokens, dtype=np.int32)
+    size = config.lookback + config.max_match_length + 1
+    hist = np.zeros(max(size, 1), dtype=np.int32)
+    nh = ctypes.c_int()
+    cap = max(size, 1)
+    pt = np.zeros(cap, dtype=np.int32)
+    pv = np.zeros(cap, dtype=np.float64)
+    n = oracle().orc_dry_run(ctypes.byref(config), _ptr(ex), len(ex), _ptr(t), len(t), _ptr(hist), ctypes.byref(nh),
+                             _ptr(pt), _ptr(pv), cap)
+    return hist[:nh.value].copy(), pt[:n].copy(), pv[:n].copy()
+
+
+def haru_shape(logits, pen_tokens, pens, silent, pad, eop, eos, eop_bias=0.0, must_speak=False):
+    out = np.ascontiguousarray(logits, dtype=np.float32).copy()
+    pt = np.ascontiguousarray(pen_tokens, dtype=np.int32)
+    pv = np.ascontiguousarray(pens, dtype=np.float64)
+    sl = np.ascontiguousarray(silent, dtype=np.float32)
+    oracle().orc_haru_shape(_ptr(out), _ptr(pt), _ptr(pv), len(pt), _ptr(sl), pad, eop, eos, eop_bias, int(must_speak))
+    return out
