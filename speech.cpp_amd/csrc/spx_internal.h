@@ -63,6 +63,7 @@ struct WideMem {
     uint64_t red[16];
     uint64_t lo_e;              // the lowest entry of the row (its last token in the order)
     uint32_t n_gath;
+    int32_t wb[2];              // the first and last bin a gathering read needs
 };
 template <int B>
 constexpr size_t wide_lds_bytes() {

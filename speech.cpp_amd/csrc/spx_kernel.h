@@ -1296,6 +1296,10 @@ struct FbRow {
     float top;  // the largest final quotient
     Red * red;
     uint32_t * n_own;
+    // A read that needs only quotients within a range: the raw logits that can reach it (a conservative window), so
+    // that every other token other than the special ones is passed over before its division. win false: every token.
+    bool win = false;
+    float wlo = -INFINITY, whi = INFINITY;
 };
 
 // Visits every token of the row, chunk by chunk: f(entry, final logit, quotient, banned, id), the entry 0 for a NaN
@@ -1311,17 +1315,22 @@ __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
     const bool spec = r.pl.pen || r.banned_row;
     const uint32_t ninf = order_key(-INFINITY);
     const int tid = threadIdx.x;
-    // one token: its special bit, then its quotient
+    // one token: its special bit, then its quotient. A special token is visited after the chunk's stream: a banned one
+    // from the ban mask's words, a history token from the list. (No other memory is read per token, so that the wait
+    // for the next step's vectors comes only at the step's end.)
     auto visit = [&](int c0, int i, float x) __attribute__((always_inline)) {
         if (spec) {
             const int o = i - c0;
-            if ((r.sp.kill[o >> 5] >> (o & 31)) & 1u) {
-                // history tokens are visited below; a banned one (history or not) here
-                if (r.banned_row && ((r.banned_row[i >> 5] >> (i & 31)) & 1u))
-                    f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
-                return;
-            }
+            if ((r.sp.kill[o >> 5] >> (o & 31)) & 1u) return;
         }
+        if (r.win && !(x >= r.wlo && x <= r.whi)) return;  // its quotient lies outside the read's range (or NaN)
+        const float q = div_rn(x, r.pl.t, r.pl.rt);
+        f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
+    };
+    // the same for a token of a vector whose special bits are known (one read of the word for the vector's V tokens)
+    auto visit_known = [&](int i, float x, bool special) __attribute__((always_inline)) {
+        if (special) return;
+        if (r.win && !(x >= r.wlo && x <= r.whi)) return;
         const float q = div_rn(x, r.pl.t, r.pl.rt);
         f(__builtin_isnan(q) ? 0ull : make_entry(order_key(q), (uint32_t) i), x, q, false, i);
     };
@@ -1339,32 +1348,50 @@ __device__ __forceinline__ void fb_visit(FbRow & r, F && f) {
         const int ng = a.vec_ok ? (c1 - c0) / V : 0;  // whole vectors
         const U32x4 * vp = (const U32x4 *) (rowp + c0);
         constexpr int per = U * B;
-        U32x4 cur[U], nxt[U];
+        // Loads are issued only here, into nxt; a step's vectors are copied out of it at the step's start (its one
+        // wait), then the next step's are requested. The first turn only requests step 0: with no load before the
+        // loop, no register the steps work in has a load pending on it when the loop is entered, and the compiler
+        // waits for memory once a step rather than at each reuse of a register.
+        U32x4 nxt[U];
 #pragma unroll
-        for (int u = 0; u < U; u++) {
-            const int g = tid + u * B;
-            cur[u] = g < ng ? vp[g] : U32x4{0u, 0u, 0u, 0u};
-        }
-        for (int g0 = 0; g0 < ng; g0 += per) {
+        for (int u = 0; u < U; u++) nxt[u] = U32x4{0u, 0u, 0u, 0u};
+        for (int g0 = -per; g0 < ng; g0 += per) {
+            U32x4 cur[U];
+#pragma unroll
+            for (int u = 0; u < U; u++) cur[u] = nxt[u];
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int g = g0 + per + tid + u * B;
                 nxt[u] = g < ng ? vp[g] : U32x4{0u, 0u, 0u, 0u};
             }
+            if (g0 < 0) continue;
 #pragma unroll
             for (int u = 0; u < U; u++) {
                 const int g = g0 + tid + u * B;
                 if (g < ng) {
                     float x[V];
                     unpack<T>(cur[u], x);
+                    // the vector's V special bits: one word holds them (V divides 32, the vector starts at a
+                    // multiple of V from c0)
+                    const uint32_t kb = spec ? r.sp.kill[(g * V) >> 5] >> ((g * V) & 31) : 0u;
 #pragma unroll
-                    for (int j = 0; j < V; j++) visit(c0, c0 + g * V + j, x[j]);
+                    for (int j = 0; j < V; j++) visit_known(c0 + g * V + j, x[j], (kb >> j) & 1u);
                 }
             }
-#pragma unroll
-            for (int u = 0; u < U; u++) cur[u] = nxt[u];
         }
         for (int i = c0 + ng * V + tid; i < c1; i += B) visit(c0, i, load_one<T>(rowp + i));
+        if (r.banned_row) {
+            // the banned tokens as -inf, once each (history or not: restricted() bans after the penalty); c0 is a
+            // multiple of 64, so the chunk's words are whole words of the mask
+            for (int w = (c0 >> 5) + tid; w < (c1 + 31) >> 5; w += B) {
+                uint32_t bw = r.banned_row[w];
+                while (bw) {
+                    const int i = (w << 5) + __builtin_ctz(bw);
+                    bw &= bw - 1u;
+                    if (i < c1) f(make_entry(ninf, (uint32_t) i), -INFINITY, -INFINITY, true, i);
+                }
+            }
+        }
         if (r.pl.pen) {
             for (int k = tid; k < r.sp.n_own; k += B) {
                 int cnt;
@@ -1653,6 +1680,22 @@ __device__ __forceinline__ int wide_bin(float q, float top) {
     return d < (float) (NB - 1) ? (int) d : NB - 1;
 }
 
+// The raw-logit window of the bins b0..b1 (NB - 1 the last finite bin, NB the -inf one): quotients in
+// (top - (b1 + 1) / 64, top - b0 / 64], widened by far more than the roundings of the bin's arithmetic and of the
+// division (2^-16 relative), then the logits whose correctly rounded quotient can fall there (the division by t > 0
+// is monotone), widened again. Tokens outside are in none of the bins.
+template <int NB>
+__device__ __forceinline__ void set_window(FbRow & r, float top, int b0, int b1) {
+    constexpr float kRel = 1.0f / 65536.0f;
+    const float slack = (__builtin_fabsf(top) + 1.0f) * kRel;
+    const float qhi = top - (float) b0 / kWideScale + slack;
+    const float qlo = b1 >= NB - 1 ? -INFINITY : top - (float) (b1 + 1) / kWideScale - slack;
+    const float t = r.pl.t;
+    r.win = true;
+    r.whi = qhi * t + __builtin_fabsf(qhi * t) * kRel + 1e-30f;
+    r.wlo = qlo == -INFINITY ? -INFINITY : qlo * t - __builtin_fabsf(qlo * t) * kRel - 1e-30f;
+}
+
 // Exclusive prefix sum of one 64-bit value per thread over the work-group; `total` gets the sum. red: LDS of B/64.
 template <int B>
 __device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t * red, uint64_t & total) {
@@ -1755,12 +1798,14 @@ __device__ __forceinline__ void gather_in_order(FbRow & r, WideMem<NB, CAP> & m,
     const uint32_t base = m.pre_cnt[b0];
     for (int b = b0 + tid; b <= b1; b += B) m.seg[b] = m.pre_cnt[b] - base;
     __syncthreads();
+    set_window<NB>(r, top, b0, b1);
     fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
         if (!e) return;
         const int b = (banned || !(qq > -INFINITY)) ? NB : wide_bin<NB>(qq, top);
         if (b < b0 || b > b1) return;
         m.ent[atomicAdd(&m.seg[b], 1u)] = e;
     });
+    r.win = false;
     __syncthreads();
     const int n = (int) (m.pre_cnt[b1 + 1] - base);
     for (int i = tid; i < n; i += B) {
@@ -1964,20 +2009,32 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
     if (tid == 0) m.lo_e = ~0ull;
     __syncthreads();
     uint64_t lo_e = ~0ull;
+    // the crowded bins, counted in registers: -inf tokens, and tokens of the last finite bin whose mass rounds to 0
+    uint32_t n_ninf = 0, n_far = 0;
     fb_visit<T, B>(r, [&](uint64_t e, float, float q, bool banned, int) {
         if (!e) return;  // NaN: none in a row that reaches here
         lo_e = e < lo_e ? e : lo_e;
         if (banned || !(q > -INFINITY)) {
-            atomicAdd(&m.pre_cnt[NB], 1u);
+            n_ninf++;
             return;
         }
         const int b = wide_bin<NB>(q, top);
-        atomicAdd(&m.pre_cnt[b], 1u);
         const uint64_t fm = fixed_mass(q, top, shift);
+        if (b == NB - 1 && !fm) {
+            n_far++;
+            return;
+        }
+        atomicAdd(&m.pre_cnt[b], 1u);
         if (fm) atomicAdd((unsigned long long *) &m.pre_mass[b], (unsigned long long) fm);
     });
     lo_e = wave_min_u64(lo_e);
-    if (lane_id() == 0) atomicMin((unsigned long long *) &m.lo_e, (unsigned long long) lo_e);
+    n_ninf = (uint32_t) wave_sum_i32((int) n_ninf);
+    n_far = (uint32_t) wave_sum_i32((int) n_far);
+    if (lane_id() == 0) {
+        atomicMin((unsigned long long *) &m.lo_e, (unsigned long long) lo_e);
+        if (n_ninf) atomicAdd(&m.pre_cnt[NB], n_ninf);
+        if (n_far) atomicAdd(&m.pre_cnt[NB - 1], n_far);
+    }
     __syncthreads();
     // prefix sums over the NB + 1 bins, each thread a contiguous run of them
     {
@@ -2178,6 +2235,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             return e != 0 && (ninf ? NB : wide_bin<NB>(qq, top)) == b;
         };
         // per sub-bin: count, mass, and the smallest and largest key (a sub-bin of one key is a run of equal tokens)
+        set_window<NB>(r, top, b, b);  // every read below takes tokens of bin b only
         uint32_t * scnt = (uint32_t *) m.ent;
         uint32_t * smin = scnt + (SNB + 1);
         uint32_t * smax = smin + SNB;
@@ -2395,13 +2453,26 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
                 __syncthreads();
             }
         }
-        // the segments of the gathered bins, in bin order
+        // the segments of the gathered bins, in bin order, and the first and last of them
+        if (tid == 0) {
+            m.wb[0] = NB + 1;
+            m.wb[1] = -1;
+        }
+        __syncthreads();
         {
             constexpr int P = (NB + 1 + B - 1) / B;
             const int b0 = min(tid * P, NB + 1), b1 = min(b0 + P, NB + 1);
-            int c = 0;
+            int c = 0, first = NB + 1, lastb = -1;
             for (int b = b0; b < b1; b++)
-                if ((m.need[b >> 5] >> (b & 31)) & 1u) c += (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
+                if ((m.need[b >> 5] >> (b & 31)) & 1u) {
+                    c += (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
+                    first = min(first, b);
+                    lastb = max(lastb, b);
+                }
+            if (lastb >= 0) {
+                atomicMin(&m.wb[0], first);
+                atomicMax(&m.wb[1], lastb);
+            }
             int tot;
             int off = block_excl_scan_i32<B>(c, r.red->i, tot);
             for (int b = b0; b < b1; b++) {
@@ -2412,6 +2483,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             __syncthreads();
         }
         // the gathering read: each token of a needed bin appended to its bin's segment with its mass
+        if (m.wb[1] >= 0) set_window<NB>(r, top, m.wb[0], m.wb[1]);
         fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
             if (!e) return;
             const bool ninf = banned || !(qq > -INFINITY);
@@ -2421,6 +2493,7 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             m.ent[pos] = e;
             m.mass[pos] = ninf ? 0ull : fixed_mass(qq, top, shift);
         });
+        r.win = false;
         __syncthreads();
         // each gathered token's rank and cumulative masses, from the tokens of its bin above it, kept in registers
         const int ng = (int) m.n_gath;
