@@ -1696,6 +1696,31 @@ __device__ __forceinline__ void set_window(FbRow & r, float top, int b0, int b1)
     r.wlo = qlo == -INFINITY ? -INFINITY : qlo * t - __builtin_fabsf(qlo * t) * kRel - 1e-30f;
 }
 
+// Sorts v[0..n) in falling order (bitonic, over the next power of two, padded with 0, below every entry); v holds at
+// least that many. Ends with a barrier.
+template <int B>
+__device__ __forceinline__ void block_sort_desc_u64(uint64_t * v, int n) {
+    int p = 1;
+    while (p < n) p <<= 1;
+    for (int i = n + (int) threadIdx.x; i < p; i += B) v[i] = 0ull;
+    for (int size = 2; size <= p; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            __syncthreads();
+            for (int i = threadIdx.x; i < (p >> 1); i += B) {
+                const int lo = 2 * i - (i & (stride - 1));
+                const int hi = lo + stride;
+                const bool down = (lo & size) == 0;
+                const uint64_t x = v[lo], y = v[hi];
+                if ((x < y) == down) {
+                    v[lo] = y;
+                    v[hi] = x;
+                }
+            }
+        }
+    }
+    __syncthreads();
+}
+
 // Exclusive prefix sum of one 64-bit value per thread over the work-group; `total` gets the sum. red: LDS of B/64.
 template <int B>
 __device__ __forceinline__ uint64_t block_excl_scan_u64(uint64_t v, uint64_t * red, uint64_t & total) {
@@ -1735,6 +1760,35 @@ struct WideQ {
 enum WideQIdx : int { kQK = 0, kQCut = 1, kQPick = 2, kQLast = 3 };
 
 // The first bin whose tokens bring the cumulative count past `rank` (pre_cnt[b] <= rank < pre_cnt[b + 1]).
+// The fixed-point mass of an entry's quotient (0 for -inf).
+__device__ __forceinline__ uint64_t entry_mass(uint64_t e, float top, int shift) {
+    const float q = entry_value(e);
+    return q > -INFINITY ? fixed_mass(q, top, shift) : 0ull;
+}
+
+// pre[i] = the masses of ent[0..i) (ent sorted, n <= CAP), each thread a run of CAP / B of them. Ends with a barrier.
+template <int B, int CAP>
+__device__ __forceinline__ void excl_mass_scan(const uint64_t * ent, uint64_t * pre, int n, float top, int shift,
+                                               uint64_t * red) {
+    constexpr int P = CAP / B;
+    const int i0 = (int) threadIdx.x * P;
+    uint64_t ms[P];
+    uint64_t sum = 0;
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        ms[j] = i0 + j < n ? entry_mass(ent[i0 + j], top, shift) : 0ull;
+        sum += ms[j];
+    }
+    uint64_t total;
+    uint64_t base = block_excl_scan_u64<B>(sum, red, total);
+#pragma unroll
+    for (int j = 0; j < P; j++) {
+        if (i0 + j < n) pre[i0 + j] = base;
+        base += ms[j];
+    }
+    __syncthreads();
+}
+
 template <int NB>
 __device__ __forceinline__ int bin_of_rank(const uint32_t * pre_cnt, uint64_t rank) {
     int lo = 0, hi = NB;  // pre_cnt[0] = 0 <= rank < pre_cnt[NB + 1]
@@ -1807,16 +1861,10 @@ __device__ __forceinline__ void gather_in_order(FbRow & r, WideMem<NB, CAP> & m,
     });
     r.win = false;
     __syncthreads();
+    // the batch's bins hold falling ranges of entries: sorted, the tokens are in the row's order
     const int n = (int) (m.pre_cnt[b1 + 1] - base);
-    for (int i = tid; i < n; i += B) {
-        const uint64_t e = m.ent[i];
-        const float qq = entry_value(e);
-        const int b = !(qq > -INFINITY) ? NB : wide_bin<NB>(qq, top);
-        const int s0 = (int) (m.pre_cnt[b] - base), s1 = (int) (m.pre_cnt[b + 1] - base);
-        int rho = 0;
-        for (int j = s0; j < s1; j++) rho += m.ent[j] > e ? 1 : 0;
-        out[s0 + rho] = e;
-    }
+    block_sort_desc_u64<B>(m.ent, n);
+    for (int i = tid; i < n; i += B) out[i] = m.ent[i];
     __syncthreads();
 }
 
@@ -2249,40 +2297,93 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             }
         }
         __syncthreads();
+        // Each thread sums the run of its tokens that fall in one sub-bin in registers and adds it when the sub-bin
+        // changes: a bin of one value (a run of equal logits) takes one set of atomics per thread, not per token.
+        int acc_sb = -1;
+        uint32_t acc_n = 0, acc_lo = ~0u, acc_hi = 0u;
+        uint64_t acc_m = 0;
+        auto flush = [&]() {
+            if (acc_sb < 0) return;
+            atomicAdd(&scnt[acc_sb], acc_n);
+            atomicMin(&smin[acc_sb], acc_lo);
+            atomicMax(&smax[acc_sb], acc_hi);
+            if (acc_m) atomicAdd((unsigned long long *) &smass[acc_sb], (unsigned long long) acc_m);
+        };
         fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
             if (!in_bin(e, qq, banned)) return;
             const int sb = sub_of(qq, id);
-            atomicAdd(&scnt[sb], 1u);
-            atomicMin(&smin[sb], entry_key(e));
-            atomicMax(&smax[sb], entry_key(e));
-            const uint64_t fm = (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
-            if (fm) atomicAdd((unsigned long long *) &smass[sb], (unsigned long long) fm);
+            if (sb != acc_sb) {
+                flush();
+                acc_sb = sb;
+                acc_n = 0;
+                acc_lo = ~0u;
+                acc_hi = 0u;
+                acc_m = 0;
+            }
+            const uint32_t key = entry_key(e);
+            acc_n++;
+            acc_lo = min(acc_lo, key);
+            acc_hi = max(acc_hi, key);
+            acc_m += (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
         });
+        flush();
         __syncthreads();
-        // the sub-bin of the target, by one lane
-        if (tid == 0) {
-            uint32_t c = m.pre_cnt[b];
-            uint64_t ms = m.pre_mass[b];
-            int sb = -1;
-            for (int j = 0; j < SNB && sb < 0; j++) {
+        // the sub-bin of the target: the first non-empty one whose running count or mass reaches it, found by every
+        // thread over its run of sub-bins from the exclusive sums before the run
+        {
+            constexpr int SP = (SNB + B - 1) / B;
+            const int j0 = tid * SP;
+            uint32_t cl = 0;
+            uint64_t ml = 0;
+            for (int k = 0; k < SP; k++)
+                if (j0 + k < SNB) {
+                    cl += scnt[j0 + k];
+                    ml += smass[j0 + k];
+                }
+            int ctot;
+            uint64_t mtot;
+            uint32_t c = m.pre_cnt[b] + (uint32_t) block_excl_scan_i32<B>((int) cl, r.red->i, ctot);
+            uint64_t ms = m.pre_mass[b] + block_excl_scan_u64<B>(ml, m.red, mtot);
+            if (tid == 0) m.wb[0] = SNB;
+            __syncthreads();
+            int sbm = SNB;
+            uint32_t cb = 0;
+            uint64_t mb = 0;
+            for (int k = 0; k < SP && sbm == SNB; k++) {
+                const int j = j0 + k;
+                if (j >= SNB) break;
                 const uint32_t c1 = c + scnt[j];
                 const uint64_t m1 = ms + smass[j];
                 bool here;
                 if (Q.kind == kQRank) here = Q.lo < (uint64_t) c1;
                 else if (Q.kind == kQGe) here = Q.lo == 0 ? true : m1 >= Q.lo;
                 else here = m1 > Q.lo;
-                if (here && scnt[j] > 0) sb = j;
-                else {
+                if (here && scnt[j] > 0) {
+                    sbm = j;
+                    cb = c;
+                    mb = ms;
+                } else {
                     c = c1;
                     ms = m1;
                 }
             }
-            m.ans[0].found = sb >= 0 ? 1u : 0u;
-            m.ans[0].rank = (uint32_t) max(sb, 0);
-            m.ans[0].before = ms;
-            m.ans[0].through = c;
-            m.n_gath = sb >= 0 ? scnt[sb] : 0u;
-            m.ans[0].entry = sb >= 0 && smin[sb] == smax[sb] ? (uint64_t) smin[sb] + 1 : 0ull;  // its one key + 1
+            if (sbm < SNB) atomicMin(&m.wb[0], sbm);
+            __syncthreads();
+            const int first = m.wb[0];
+            if (tid == 0 && first == SNB) {
+                m.ans[0].found = 0u;
+                m.ans[0].rank = 0u;
+                m.n_gath = 0u;
+                m.ans[0].entry = 0ull;
+            }
+            if (sbm < SNB && sbm == first) {
+                m.ans[0].found = 1u;
+                m.ans[0].rank = (uint32_t) sbm;
+                m.ans[0].before = mb;
+                m.ans[0].through = cb;
+                m.n_gath = scnt[sbm];
+                m.ans[0].entry = smin[sbm] == smax[sbm] ? (uint64_t) smin[sbm] + 1 : 0ull;  // its one key + 1
+            }
         }
         __syncthreads();
         const int sb = (int) m.ans[0].rank;
@@ -2318,13 +2419,32 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
                 if (in_bin(e, qq, banned) && entry_key(e) == key) atomicAdd(&scnt[idbin(id)], 1u);
             });
             __syncthreads();
-            if (tid == 0) {
-                uint32_t c = 0;
-                int ib = 0;
-                while (ib < SNB - 1 && (uint64_t) (c + scnt[ib]) <= j) c += scnt[ib++];
-                m.ans[0].rank = (uint32_t) ib;
-                m.ans[0].through = c;
-                m.n_gath = 0u;
+            {
+                // the id range holding place j of the run: the first whose running count passes j (the last one where
+                // none does), every thread over its run of ranges
+                constexpr int SP = (SNB + B - 1) / B;
+                const int i0 = tid * SP;
+                uint32_t cl = 0;
+                for (int k = 0; k < SP; k++)
+                    if (i0 + k < SNB) cl += scnt[i0 + k];
+                int ctot;
+                uint32_t c = (uint32_t) block_excl_scan_i32<B>((int) cl, r.red->i, ctot);
+                if (tid == 0) m.wb[0] = SNB - 1;
+                __syncthreads();
+                int ibm = SNB;
+                for (int k = 0; k < SP && ibm == SNB; k++) {
+                    const int ib = i0 + k;
+                    if (ib >= SNB) break;
+                    if (ib == SNB - 1 || (uint64_t) (c + scnt[ib]) > j) ibm = ib;
+                    else c += scnt[ib];
+                }
+                if (ibm < SNB) atomicMin(&m.wb[0], ibm);
+                __syncthreads();
+                if (ibm < SNB && ibm == m.wb[0]) {
+                    m.ans[0].rank = (uint32_t) ibm;
+                    m.ans[0].through = c;
+                    m.n_gath = 0u;
+                }
             }
             __syncthreads();
             const int ib = (int) m.ans[0].rank;
@@ -2339,14 +2459,10 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             });
             __syncthreads();
             const int n2 = (int) m.n_gath;
-            for (int x = tid; x < n2; x += B) {
-                const uint64_t e = m.ent[x];
-                uint32_t rho = 0;
-                for (int y = 0; y < n2; y++) rho += m.ent[y] > e ? 1u : 0u;
-                if ((uint64_t) rho == jb) {
-                    m.ans[0].entry = e;
-                    m.ans[0].found = 1u;
-                }
+            block_sort_desc_u64<B>(m.ent, n2);
+            if (tid == 0 && jb < (uint64_t) n2) {
+                m.ans[0].entry = m.ent[jb];
+                m.ans[0].found = 1u;
             }
             __syncthreads();
             if (!m.ans[0].found) return false;
@@ -2363,23 +2479,16 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
         __syncthreads();
         fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int id) {
             if (!in_bin(e, qq, banned) || sub_of(qq, id) != sb) return;
-            const uint32_t pos = atomicAdd(&m.n_gath, 1u);
-            m.ent[pos] = e;
-            m.mass[pos] = (banned || !(qq > -INFINITY)) ? 0ull : fixed_mass(qq, top, shift);
+            m.ent[atomicAdd(&m.n_gath, 1u)] = e;
         });
         for (int t = tid; t < kWideQs; t += B) m.ans[t].found = 0u;
         __syncthreads();
+        block_sort_desc_u64<B>(m.ent, ng);
+        excl_mass_scan<B, CAP>(m.ent, m.mass, ng, top, shift, m.red);
         for (int x = tid; x < ng; x += B) {
             const uint64_t e = m.ent[x];
-            uint32_t rho = 0;
-            uint64_t mu = 0;
-            for (int j = 0; j < ng; j++) {
-                if (m.ent[j] > e) {
-                    rho++;
-                    mu += m.mass[j];
-                }
-            }
-            const uint64_t rank = base_c + rho, before = base_m + mu, through = before + m.mass[x];
+            const uint64_t rank = base_c + (uint64_t) x, before = base_m + m.mass[x];
+            const uint64_t through = before + entry_mass(e, top, shift);
             bool hit;
             if (Q.kind == kQRank) hit = rank == Q.lo;
             else if (Q.kind == kQGe) hit = Q.lo == 0 ? rank == 0 : (before < Q.lo && Q.lo <= through);
@@ -2482,21 +2591,23 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             if (tid == 0) m.n_gath = (uint32_t) tot;
             __syncthreads();
         }
-        // the gathering read: each token of a needed bin appended to its bin's segment with its mass
+        // the gathering read: each token of a needed bin appended to its bin's segment
         if (m.wb[1] >= 0) set_window<NB>(r, top, m.wb[0], m.wb[1]);
         fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
             if (!e) return;
             const bool ninf = banned || !(qq > -INFINITY);
             const int b = ninf ? NB : wide_bin<NB>(qq, top);
             if (!((m.need[b >> 5] >> (b & 31)) & 1u)) return;
-            const uint32_t pos = atomicAdd(&m.seg[b], 1u);
-            m.ent[pos] = e;
-            m.mass[pos] = ninf ? 0ull : fixed_mass(qq, top, shift);
+            m.ent[atomicAdd(&m.seg[b], 1u)] = e;  // its mass follows from the entry once sorted
         });
         r.win = false;
         __syncthreads();
         // each gathered token's rank and cumulative masses, from the tokens of its bin above it, kept in registers
         const int ng = (int) m.n_gath;
+        // sorted, the gathered bins keep their segments (a bin holds a falling range of entries), each in the row's
+        // order; the masses' running sums give each token's mass above it
+        block_sort_desc_u64<B>(m.ent, ng);
+        excl_mass_scan<B, CAP>(m.ent, m.mass, ng, top, shift, m.red);
         uint64_t te[TPT], tbefore[TPT], tthrough[TPT], trank[TPT];
 #pragma unroll
         for (int x = 0; x < TPT; x++) {
@@ -2508,20 +2619,11 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             const uint64_t e = m.ent[i];
             const float qq = entry_value(e);
             const int b = !(qq > -INFINITY) ? NB : wide_bin<NB>(qq, top);
-            const int s1 = (int) m.seg[b], s0 = s1 - (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
-            uint32_t rho = 0;
-            uint64_t mu = 0;
-            for (int j = s0; j < s1; j++) {
-                const uint64_t f = m.ent[j];
-                if (f > e) {
-                    rho++;
-                    mu += m.mass[j];
-                }
-            }
+            const int s0 = (int) m.seg[b] - (int) (m.pre_cnt[b + 1] - m.pre_cnt[b]);
             te[x] = e;
-            trank[x] = (uint64_t) m.pre_cnt[b] + rho;
-            tbefore[x] = m.pre_mass[b] + mu;
-            tthrough[x] = tbefore[x] + m.mass[i];
+            trank[x] = (uint64_t) m.pre_cnt[b] + (uint64_t) (i - s0);
+            tbefore[x] = m.pre_mass[b] + (m.mass[i] - m.mass[s0]);
+            tthrough[x] = tbefore[x] + entry_mass(e, top, shift);
         }
         // answer every question the gathered tokens can, as long as answers make more targets known
         for (int step = 0; step < kWideQs + 1; step++) {
