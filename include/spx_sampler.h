@@ -244,6 +244,19 @@ spx_status spx_haru_shape_rows(float * d_logits, int rows, int vocab, int64_t ld
                                float eop_bias, const uint8_t * d_must_speak, int32_t * d_out_pen_tokens,
                                double * d_out_pen, int32_t * d_out_npen, int pen_cap, void * stream);
 
+/*
+ * The LM head's pick fused with its product: Qwen3Decoder::outputs() with Qwen3Readback::Pick
+ * (src/common/qwen3-decoder.cpp:422-429) and verify()'s picks (:497-501). For each of `rows` hidden states (fp32, rows
+ * hidden_ld floats apart): ggml's rms_norm with eps, times d_norm_weight (null: 1), the product with the head (vocab
+ * rows of d bf16 weights, head_ld elements apart, 16-byte aligned; d a multiple of 16) in bf16 on the matrix cores
+ * with fp32 sums, and the first largest logit (a NaN before any number, as torch.argmax): d_out_ids[r], and that
+ * logit in d_out_max[r] (may be null). The logits never reach memory. At most 64 rows, and rows * d * 2 bytes within
+ * the handle's workspace (8 KiB per row of max_rows).
+ */
+spx_status spx_head_argmax_rows(spx_sampler * s, const float * d_hidden, int64_t hidden_ld, const float * d_norm_weight,
+                                float eps, const uint16_t * d_head, int64_t head_ld, int rows, int d, int vocab,
+                                int32_t * d_out_ids, float * d_out_max, void * stream);
+
 /* Rows per call of spx_sample_rows_noalloc. */
 #define SPX_NOALLOC_MAX_ROWS 2048
 

@@ -33,7 +33,7 @@ assert ROW_PARAMS.itemsize == 32
 EXPORTS = ["spx_sampler_create", "spx_sampler_destroy", "spx_sample_rows", "spx_argmax_rows", "spx_candidates_rows",
            "spx_sample_chain",
            "spx_drama3_main", "spx_talker_bans", "spx_last_error", "spx_sampler_last_stats", "spx_sample_rows_noalloc",
-           "spx_dry_update_rows", "spx_haru_shape_rows"]
+           "spx_dry_update_rows", "spx_haru_shape_rows", "spx_head_argmax_rows"]
 
 
 class DryConfig(ctypes.Structure):
@@ -91,6 +91,8 @@ def load_library(path=LIB_PATH):
     lib.spx_haru_shape_rows.argtypes = [vp, i32, i32, i64, ctypes.POINTER(DryConfig), vp, i32, vp, vp, i32, vp, i32,
                                         i32, i32, ctypes.c_float, vp, vp, vp, vp, i32, vp]
     lib.spx_haru_shape_rows.restype = i32
+    lib.spx_head_argmax_rows.argtypes = [p, vp, i64, vp, ctypes.c_float, vp, i64, i32, i32, i32, vp, vp, vp]
+    lib.spx_head_argmax_rows.restype = i32
     _lib = lib
     return lib
 
@@ -237,6 +239,23 @@ class Sampler:
                                              semantic_begin, semantic_end, window, _ptr(hist), _ptr(hist_off),
                                              _ptr(out_ids), _ptr(out_status), ctypes.c_void_p(s)))
         return out_ids, out_status
+
+    def head_argmax(self, hidden, norm_weight, eps, head, out_ids=None, out_max=None, stream=None):
+        """The fused LM-head pick: hidden (rows x d float32), norm_weight (d float32 or None), head (vocab x d
+        bfloat16, device tensors). Returns (ids, max logits)."""
+        import torch
+        rows, d = hidden.shape
+        vocab = head.shape[0]
+        dev = hidden.device
+        if out_ids is None:
+            out_ids = torch.empty(rows, dtype=torch.int32, device=dev)
+        if out_max is None:
+            out_max = torch.empty(rows, dtype=torch.float32, device=dev)
+        s = stream if stream is not None else torch.cuda.current_stream(dev).cuda_stream
+        self._check(self.lib.spx_head_argmax_rows(self.handle, _ptr(hidden), hidden.stride(0), _ptr(norm_weight), eps,
+                                                  _ptr(head), head.stride(0), rows, d, vocab, _ptr(out_ids),
+                                                  _ptr(out_max), ctypes.c_void_p(s)))
+        return out_ids, out_max
 
     def last_stats(self):
         st = SpxStats()

@@ -493,6 +493,38 @@ spx_status spx_haru_shape_rows(float * d_logits, int rows, int vocab, int64_t ld
     return e == hipSuccess ? SPX_OK : hip_fail(e, "haru_shape launch");
 }
 
+spx_status spx_head_argmax_rows(spx_sampler * s, const float * d_hidden, int64_t hidden_ld, const float * d_norm_weight,
+                                float eps, const uint16_t * d_head, int64_t head_ld, int rows, int d, int vocab,
+                                int32_t * d_out_ids, float * d_out_max, void * stream) {
+    using namespace spx;
+    if (!s) return fail(SPX_ERR_INVALID_ARGUMENT, "null sampler handle");
+    if (rows < 0 || rows > kHeadMaxRows || rows > s->max_rows) return fail(SPX_ERR_INVALID_ARGUMENT, "rows outside [0, min(64, max_rows)]");
+    if (d <= 0 || d % 16 != 0 || vocab <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "d must be a positive multiple of 16, vocab positive");
+    if (hidden_ld < d || head_ld < d || head_ld % 8 != 0) return fail(SPX_ERR_INVALID_ARGUMENT, "hidden_ld or head_ld below d, or head_ld not a multiple of 8");
+    if ((size_t) rows * (size_t) d * 2 > ws_cands(s->max_rows))
+        return fail(SPX_ERR_INVALID_ARGUMENT, "rows x d bf16 exceed the handle's workspace");
+    if (rows == 0) return SPX_OK;
+    if (!d_hidden || !d_head || !d_out_ids) return fail(SPX_ERR_INVALID_ARGUMENT, "null hidden, head or out_ids");
+    if ((uintptr_t) d_head % 16 != 0) return fail(SPX_ERR_INVALID_ARGUMENT, "head not 16-byte aligned");
+    HeadArgs h{};
+    h.hidden = d_hidden;
+    h.hidden_ld = hidden_ld;
+    h.norm_w = d_norm_weight;
+    h.eps = eps;
+    h.head = d_head;
+    h.head_ld = head_ld;
+    h.rows = rows;
+    h.d = d;
+    h.vocab = vocab;
+    h.max_groups = 8 * s->cus;
+    h.hn = (uint16_t *) s->base.part_cands;   // rows x d bf16: within the published candidates' region
+    h.keys = (uint64_t *) s->base.partials;   // rows picks: within the partials' region
+    h.out_ids = d_out_ids;
+    h.out_max = d_out_max;
+    const hipError_t e = launch_head_pick(h, (hipStream_t) stream);
+    return e == hipSuccess ? SPX_OK : hip_fail(e, "head pick launch");
+}
+
 spx_status spx_sampler_last_stats(spx_sampler * s, spx_stats * out) {
     if (!s || !out) return fail(SPX_ERR_INVALID_ARGUMENT, "null argument");
     int32_t c = 0;

@@ -207,6 +207,23 @@ struct DryArgs {
     double table[kDryTable];
 };
 
+// The fused head pick (spx_head.hip): its operands, the normalized hidden states and the pick keys in the handle's
+// workspace, and the work-groups the product launches at most (each loops over vocabulary tiles).
+constexpr int kHeadMaxRows = 64;
+struct HeadArgs {
+    const float * hidden;
+    int64_t hidden_ld;
+    const float * norm_w;
+    float eps;
+    const uint16_t * head;
+    int64_t head_ld;
+    int rows, d, vocab, max_groups;
+    uint16_t * hn;
+    uint64_t * keys;
+    int32_t * out_ids;
+    float * out_max;
+};
+
 // spx_api.cpp's pieces of the no-alloc entry (spx_noalloc.hip): its error messages, a handle of static storage over
 // a workspace the caller owns, and the per-call limits of such a handle.
 spx_status report(spx_status s, const char * msg);  // sets spx_last_error()'s message
@@ -215,6 +232,7 @@ spx_status bind_scratch(int device, void * ws, int max_rows, spx_sampler ** out)
 void set_call_limits(spx_sampler * s, int vocab, int max_hist, int max_out);
 spx_status dry_args(DryArgs & d, const spx_dry_config * c, const int32_t * exempt, int n_exempt, int hist_stride);
 hipError_t launch_dry_update(const DryArgs & d, hipStream_t s);
+hipError_t launch_head_pick(const HeadArgs & h, hipStream_t s);
 hipError_t launch_haru_shape(const DryArgs & d, hipStream_t s);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);

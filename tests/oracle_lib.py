@@ -218,3 +218,30 @@ def haru_shape(logits, pen_tokens, pens, silent, pad, eop, eos, eop_bias=0.0, mu
     sl = np.ascontiguousarray(silent, dtype=np.float32)
     oracle().orc_haru_shape(_ptr(out), _ptr(pt), _ptr(pv), len(pt), _ptr(sl), pad, eop, eos, eop_bias, int(must_speak))
     return out
+
+
+def bf16_round(x):
+    """float32 -> the float32 values of their bfloat16 rounding (to nearest even; NaN kept)."""
+    u = np.ascontiguousarray(x, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16
+    out = r.astype(np.uint32).view(np.float32)
+    return np.where(np.isnan(x), np.float32(np.nan), out)
+
+
+def head_pick(hidden, norm_w, eps, head_bits):
+    """The pick of Qwen3Decoder::outputs() (src/common/qwen3-decoder.cpp:422-429) on the CPU: ggml's rms_norm (a double
+    sum of squares, the mean as float, scale = 1 / sqrtf(mean + eps), x * scale in float) times the norm weight in
+    float, rounded to bf16 as ggml's product with bf16 weights converts its operand; the products with the bf16 head
+    summed in double; the first largest (np.argmax: a NaN first). Returns (ids, logits rows x vocab, abs sums)."""
+    x = np.ascontiguousarray(hidden, dtype=np.float32)
+    d = x.shape[1]
+    mean = ((x.astype(np.float64) ** 2).sum(1) / d).astype(np.float32)
+    scale = (np.float32(1.0) / np.sqrt(mean + np.float32(eps))).astype(np.float32)
+    y = (x * scale[:, None]).astype(np.float32)
+    if norm_w is not None:
+        y = (y * np.asarray(norm_w, dtype=np.float32)[None, :]).astype(np.float32)
+    hb = bf16_round(y).astype(np.float64)
+    h = (np.ascontiguousarray(head_bits, dtype=np.uint16).astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    logits = hb @ h.T
+    absum = np.abs(hb) @ np.abs(h).T
+    return np.argmax(logits, axis=1).astype(np.int32), logits, absum
