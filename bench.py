@@ -9,6 +9,8 @@ bytes per launch over its average launch time, from HIP events recorded on the l
 the oracle (a C++ restatement of the reference's sampler) timed on a bounded sample of the same rows on this host.
 
 usage: python bench.py [--gpus 1] [--steps 200] [--warmup 20] [--workload haru] [--cpu-rows 48] [--no-cpu]
+       python bench.py --lds-peak                   the LDS read bandwidth of the device (the peak the rows small
+                                                   enough for LDS are rated against)
        python bench.py --copy-mb 512 [--steps 20]   a plain device-to-device copy of known size (calibrates the
                                                    FETCH_SIZE / WRITE_SIZE counters)
        python bench.py --pmc-summary counter_collection.csv   per-kernel dispatch averages of a rocprofv3 --pmc run
@@ -33,6 +35,7 @@ WORKLOAD_LABELS = {
     "mixed": "heterogeneous mixed batch: 2048 x 151936 bf16, per-row T/top-k/top-p, hist U[0,2048], 1% greedy",
     "predictor": "Qwen3-TTS code-predictor batch: 480 x 2048 fp32, hist 64, rep 1.05, T 0.9, top-k 50",
     "talker": "Qwen3-TTS talker step: 1 x 3072 fp32, hist 128, rep 1.05, T 0.9, top-k 50",
+    "head": "LM-head pick fused with its product: 64 hidden rows x 2048 fp32, RMS norm, bf16 head 151936 x 2048, argmax",
 }
 
 
@@ -47,7 +50,82 @@ def parse():
     ap.add_argument("--seed", type=int, default=1234)
     ap.add_argument("--copy-mb", type=int, default=0)
     ap.add_argument("--pmc-summary", default=None)
+    ap.add_argument("--lds-peak", action="store_true")
     return ap.parse_args()
+
+
+def head_bench(args):
+    """The fused LM-head pick (spx_head_argmax_rows) on 64 hidden rows of 2048 against a 151936 x 2048 bf16 head
+    (several copies cycled, past the last-level cache), and the unfused path beside it: torch's bf16 product written as
+    logits, then torch.argmax."""
+    import torch
+    import workloads
+    spx = workloads.spx_module()
+    rows, d, vocab = 64, 2048, 151936
+    g = torch.Generator(device="cuda").manual_seed(args.seed)
+    hidden = torch.randn(rows, d, device="cuda", generator=g)
+    w = torch.rand(d, device="cuda", generator=g) + 0.5
+    heads = [(torch.randn(vocab, d, device="cuda", generator=g) * 0.05).to(torch.bfloat16) for _ in range(2)]
+    s = spx.Sampler(max_rows=rows, max_vocab=16, max_hist=0, max_out=0)
+    ids = torch.empty(rows, dtype=torch.int32, device="cuda")
+    mx = torch.empty(rows, dtype=torch.float32, device="cuda")
+    stream = torch.cuda.current_stream()
+    calls = [0]
+
+    def fused():
+        s.head_argmax(hidden, w, 1e-6, heads[calls[0] % 2], out_ids=ids, out_max=mx, stream=stream.cuda_stream)
+        calls[0] += 1
+
+    def unfused():
+        hn = torch.nn.functional.rms_norm(hidden, (d,), w, 1e-6).to(torch.bfloat16)
+        torch.argmax(hn @ heads[calls[0] % 2].t(), dim=1)
+        calls[0] += 1
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        st = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        en = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            st[i].record(stream)
+            fn()
+            en[i].record(stream)
+        torch.cuda.synchronize()
+        return time.perf_counter() - t0, statistics.mean(a.elapsed_time(b) for a, b in zip(st, en))
+
+    elapsed, launch_ms = timed(fused)
+    _, unfused_ms = timed(unfused)
+    algo = vocab * d * 2 + rows * d * 4 + d * 4 + rows * 8
+    achieved = algo / (launch_ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "fused LM-head pick: hidden rows/sec + achieved HBM GB/s on the head, 1 MI355X", "value":
+        rows * args.steps / elapsed, "unit": "rows/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": elapsed * 1e3 / args.steps, "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16", "data": "synthetic (random hidden states and head)",
+        "config": {"workload": WORKLOAD_LABELS["head"], "rows": rows, "d": d, "vocab": vocab},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None, "algorithmic_bytes_per_launch": algo,
+                     "launch_ms": launch_ms},
+        "unfused_torch_ms": unfused_ms}))
+
+
+def lds_peak():
+    """The device's LDS read bandwidth in GB/s, measured by speech.cpp_amd/lib/libspx_ldspeak.so: 512 work-groups of
+    1024 lanes reading conflict-free 16-byte words of a 64 KiB LDS array (median of 7 launches)."""
+    import ctypes
+    import torch  # noqa: F401  (the library binds to the HIP runtime torch loaded)
+    path = os.path.join(ROOT, "speech.cpp_amd", "lib", "libspx_ldspeak.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built (make -C speech.cpp_amd)")
+    lib = ctypes.CDLL(path)
+    lib.spx_lds_peak.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_double)]
+    lib.spx_lds_peak.restype = ctypes.c_int
+    gbs = ctypes.c_double()
+    if lib.spx_lds_peak(512, 4096, 7, ctypes.byref(gbs)) != 0:
+        raise RuntimeError("the LDS bandwidth kernel failed")
+    return gbs.value
 
 
 def copy_calibration(mb, steps, warmup):
@@ -139,6 +217,12 @@ def main():
     if args.copy_mb:
         copy_calibration(args.copy_mb, args.steps, args.warmup)
         return
+    if args.lds_peak:
+        print(json.dumps({"lds_read_peak_gbs": lds_peak()}))
+        return
+    if args.workload == "head":
+        head_bench(args)
+        return
     import torch
     import gpu_harness
     import workloads
@@ -216,6 +300,11 @@ def main():
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": algo_bytes, "launch_ms": launch_ms},
     }
+    if batch_bytes <= 64 * 1024 * rows:
+        # rows small enough for LDS (a 3072-token fp32 row is 12 KiB): the same bytes against the measured LDS peak
+        peak = lds_peak()
+        line["lds_bound"] = {"achieved": achieved, "peak": peak, "unit": "GB/s", "frac": achieved / peak,
+                             "us_per_call_events": launch_ms * 1e3, "us_per_call_wall": elapsed * 1e6 / args.steps}
     if not args.no_cpu:
         cores = host_cores()
         n = min(args.cpu_rows, rows)

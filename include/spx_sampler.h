@@ -248,7 +248,7 @@ spx_status spx_haru_shape_rows(float * d_logits, int rows, int vocab, int64_t ld
  * The LM head's pick fused with its product: Qwen3Decoder::outputs() with Qwen3Readback::Pick
  * (src/common/qwen3-decoder.cpp:422-429) and verify()'s picks (:497-501). For each of `rows` hidden states (fp32, rows
  * hidden_ld floats apart): ggml's rms_norm with eps, times d_norm_weight (null: 1), the product with the head (vocab
- * rows of d bf16 weights, head_ld elements apart, 16-byte aligned; d a multiple of 16) in bf16 on the matrix cores
+ * rows of d bf16 weights, head_ld elements apart, 16-byte aligned; d a multiple of 64) in bf16 on the matrix cores
  * with fp32 sums, and the first largest logit (a NaN before any number, as torch.argmax): d_out_ids[r], and that
  * logit in d_out_max[r] (may be null). The logits never reach memory. At most 64 rows, and rows * d * 2 bytes within
  * the handle's workspace (8 KiB per row of max_rows).

@@ -499,7 +499,7 @@ spx_status spx_head_argmax_rows(spx_sampler * s, const float * d_hidden, int64_t
     using namespace spx;
     if (!s) return fail(SPX_ERR_INVALID_ARGUMENT, "null sampler handle");
     if (rows < 0 || rows > kHeadMaxRows || rows > s->max_rows) return fail(SPX_ERR_INVALID_ARGUMENT, "rows outside [0, min(64, max_rows)]");
-    if (d <= 0 || d % 16 != 0 || vocab <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "d must be a positive multiple of 16, vocab positive");
+    if (d <= 0 || d % 64 != 0 || vocab <= 0) return fail(SPX_ERR_INVALID_ARGUMENT, "d must be a positive multiple of 64, vocab positive");
     if (hidden_ld < d || head_ld < d || head_ld % 8 != 0) return fail(SPX_ERR_INVALID_ARGUMENT, "hidden_ld or head_ld below d, or head_ld not a multiple of 8");
     if ((size_t) rows * (size_t) d * 2 > ws_cands(s->max_rows))
         return fail(SPX_ERR_INVALID_ARGUMENT, "rows x d bf16 exceed the handle's workspace");
@@ -516,7 +516,6 @@ spx_status spx_head_argmax_rows(spx_sampler * s, const float * d_hidden, int64_t
     h.rows = rows;
     h.d = d;
     h.vocab = vocab;
-    h.max_groups = 8 * s->cus;
     h.hn = (uint16_t *) s->base.part_cands;   // rows x d bf16: within the published candidates' region
     h.keys = (uint64_t *) s->base.partials;   // rows picks: within the partials' region
     h.out_ids = d_out_ids;

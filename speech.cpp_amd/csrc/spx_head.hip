@@ -66,56 +66,84 @@ __global__ __launch_bounds__(256) void head_prep_kernel(const float * hidden, in
     if (tid == 0) keys[r] = 0ull;
 }
 
-// The product and the pick. hn: rows x d bf16 (d a multiple of 16), head: vocab rows of ld bf16, 16-byte aligned.
-// COLS: 32-row column tiles (1 for up to 32 rows, 2 for up to 64).
+// The product and the pick. hn: rows x d bf16 (d a multiple of 64), head: vocab rows of ld bf16, 16-byte aligned.
+// COLS: 32-row column tiles (1 for up to 32 rows, 2 for up to 64). Each wave takes a 32-token tile of the vocabulary;
+// the work-group's four waves share the hidden rows' blocks of 64, which its threads bring into LDS a turn ahead, so
+// that a wave's loads from memory are its tile's only.
 template <int COLS>
 __global__ __launch_bounds__(kHeadThreads) void head_pick_kernel(const uint16_t * head, int64_t ld, const uint16_t * hn,
                                                                  int rows, int d, int vocab, uint64_t * keys) {
+    constexpr int kPitch = 9;  // 16-byte words per hidden row in LDS (8 used; the ninth spreads the rows over banks)
+    __shared__ uint4 bs[2][64 * kPitch];
     __shared__ uint64_t wbest[kHeadWaves][64];
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
     const int m = lane & 31, half = lane >> 5;
     const int tiles = (vocab + kTileM - 1) / kTileM;
-    uint64_t best0 = 0ull, best1 = 0ull;  // this lane's best of hidden rows m and 32 + m over its tiles
-    const bool b0ok = m < rows, b1ok = 32 + m < rows;
-    const uint4 * hb0 = (const uint4 *) (hn + (int64_t) (b0ok ? m : 0) * d);
-    const uint4 * hb1 = (const uint4 *) (hn + (int64_t) (b1ok ? 32 + m : 0) * d);
-    for (int t = blockIdx.x * kHeadWaves + wave; t < tiles; t += gridDim.x * kHeadWaves) {
-        const int v0 = t * kTileM;
-        const int va = v0 + m;
-        const bool aok = va < vocab;
-        const uint4 * ap = (const uint4 *) (head + (int64_t) (aok ? va : 0) * ld);
-        f32x16 acc0 = {}, acc1 = {};
-        // lane (m, half) holds elements kb + 8*half .. +7 of its rows: the first four to one MFMA, the last four to
-        // the next (the same split on both operands, so each product pairs the same k). Four blocks of 16 a turn,
-        // their loads issued together.
-        auto mac = [&](const uint4 & a, const uint4 & b, const uint4 & c) __attribute__((always_inline)) {
-            const bf16x4 alo = __builtin_bit_cast(bf16x4, make_uint2(a.x, a.y));
-            const bf16x4 ahi = __builtin_bit_cast(bf16x4, make_uint2(a.z, a.w));
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(alo, __builtin_bit_cast(bf16x4, make_uint2(b.x, b.y)), acc0, 0, 0, 0);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ahi, __builtin_bit_cast(bf16x4, make_uint2(b.z, b.w)), acc0, 0, 0, 0);
-            if (COLS > 1) {
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(alo, __builtin_bit_cast(bf16x4, make_uint2(c.x, c.y)), acc1, 0, 0, 0);
-                acc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ahi, __builtin_bit_cast(bf16x4, make_uint2(c.z, c.w)), acc1, 0, 0, 0);
-            }
-        };
-        const uint4 z = make_uint4(0u, 0u, 0u, 0u);
-        int kb = 0;
-        for (; kb + 64 <= d; kb += 64) {
-            uint4 a[4], b[4], c[4];
+    const int t = blockIdx.x * kHeadWaves + wave;  // this wave's tile (past the last: it only helps with the loads)
+    const int v0 = t * kTileM;
+    // tokens past the vocabulary read its last row, hidden rows past the batch the batch's last (every load in
+    // bounds); their products are never taken
+    const uint4 * __restrict__ ap = (const uint4 *) (head + (int64_t) min(v0 + m, vocab - 1) * ld);
+    // the work-group's share of a turn's hidden blocks: 64 rows x 8 words, two words a thread
+    const int e0 = tid, e1 = tid + kHeadThreads;
+    const uint4 * __restrict__ hp0 = (const uint4 *) (hn + (int64_t) min(e0 >> 3, rows - 1) * d) + (e0 & 7);
+    const uint4 * __restrict__ hp1 = (const uint4 *) (hn + (int64_t) min(e1 >> 3, rows - 1) * d) + (e1 & 7);
+    f32x16 acc0 = {}, acc1 = {};
+    auto mac = [&](const uint4 & a, const uint4 & b, const uint4 & c) __attribute__((always_inline)) {
+        const bf16x4 alo = __builtin_bit_cast(bf16x4, make_uint2(a.x, a.y));
+        const bf16x4 ahi = __builtin_bit_cast(bf16x4, make_uint2(a.z, a.w));
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(alo, __builtin_bit_cast(bf16x4, make_uint2(b.x, b.y)), acc0, 0, 0, 0);
+        acc0 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ahi, __builtin_bit_cast(bf16x4, make_uint2(b.z, b.w)), acc0, 0, 0, 0);
+        if (COLS > 1) {
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(alo, __builtin_bit_cast(bf16x4, make_uint2(c.x, c.y)), acc1, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(ahi, __builtin_bit_cast(bf16x4, make_uint2(c.z, c.w)), acc1, 0, 0, 0);
+        }
+    };
+    // Turns of 64: lane (m, half) holds elements 16*j + 8*half .. +7 of its rows for j < 4, the first four of each to
+    // one MFMA and the last four to the next (the same split on both operands, so each product pairs the same k).
+    // Turn k computes from its LDS buffer k % 2 with the tile's words loaded a turn ahead; the hidden blocks of turn
+    // k + 1, loaded a turn ahead too, go to the other buffer meanwhile. Loads go only to the `n` registers, and the
+    // first pass (k = -1) only issues them and fills buffer 0, so no register in use has a load pending on it.
+    const int turns = d >> 6;
+    uint4 na[4], nh0, nh1;
+#pragma unroll
+    for (int j = 0; j < 4; j++) na[j] = make_uint4(0u, 0u, 0u, 0u);
+    nh0 = nh1 = make_uint4(0u, 0u, 0u, 0u);
+    for (int k = -1; k < turns; k++) {
+        uint4 a[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) a[j] = na[j];
+        const uint4 h0 = nh0, h1 = nh1;  // turn k + 1's hidden blocks (k >= 0)
+        if (k + 1 < turns) {
+            const int q = (k + 1) * 8;  // turn k + 1's first 16-byte word of a row
+#pragma unroll
+            for (int j = 0; j < 4; j++) na[j] = ap[q + 2 * j + half];
+        }
+        if (k + 2 < turns) {
+            nh0 = hp0[(k + 2) * 8];
+            nh1 = hp1[(k + 2) * 8];
+        }
+        if (k >= 0) {
+            const uint4 * b = bs[k & 1];
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const int q = ((kb + 16 * j) >> 3) + half;  // 16-byte index within the row
-                a[j] = aok ? ap[q] : z;
-                b[j] = b0ok ? hb0[q] : z;
-                c[j] = (COLS > 1 && b1ok) ? hb1[q] : z;
+                const uint4 b0 = b[m * kPitch + 2 * j + half];
+                const uint4 b1 = COLS > 1 ? b[(32 + m) * kPitch + 2 * j + half] : b0;
+                mac(a[j], b0, b1);
             }
-#pragma unroll
-            for (int j = 0; j < 4; j++) mac(a[j], b[j], c[j]);
         }
-        for (; kb < d; kb += 16) {
-            const int q = (kb >> 3) + half;
-            mac(aok ? ap[q] : z, b0ok ? hb0[q] : z, (COLS > 1 && b1ok) ? hb1[q] : z);
+        if (k == -1) {
+            bs[0][(e0 >> 3) * kPitch + (e0 & 7)] = hp0[0];
+            bs[0][(e1 >> 3) * kPitch + (e1 & 7)] = hp1[0];
+        } else if (k + 1 < turns) {
+            uint4 * bn = bs[(k + 1) & 1];  // last read by turn k - 1, before the barrier that ended it
+            bn[(e0 >> 3) * kPitch + (e0 & 7)] = h0;
+            bn[(e1 >> 3) * kPitch + (e1 & 7)] = h1;
         }
+        __syncthreads();
+    }
+    uint64_t best0 = 0ull, best1 = 0ull;  // this lane's best of hidden rows m and 32 + m
+    if (t < tiles) {
         // output i of lane (m, half): vocabulary row 8*(i/4) + 4*half + i%4 of the tile, hidden row m (of the tile)
 #pragma unroll
         for (int i = 0; i < 16; i++) {
@@ -170,7 +198,7 @@ hipError_t launch_head_pick(const HeadArgs & h, hipStream_t s) {
     if (e != hipSuccess) return e;
     const int tiles = (h.vocab + kTileM - 1) / kTileM;
     const int groups = (tiles + kHeadWaves - 1) / kHeadWaves;
-    const dim3 grid(groups < h.max_groups ? groups : h.max_groups);
+    const dim3 grid(groups);
     if (h.rows > 32)
         hipLaunchKernelGGL(head_pick_kernel<2>, grid, dim3(kHeadThreads), 0, s, h.head, h.head_ld, h.hn, h.rows, h.d,
                            h.vocab, h.keys);

@@ -207,8 +207,8 @@ struct DryArgs {
     double table[kDryTable];
 };
 
-// The fused head pick (spx_head.hip): its operands, the normalized hidden states and the pick keys in the handle's
-// workspace, and the work-groups the product launches at most (each loops over vocabulary tiles).
+// The fused head pick (spx_head.hip): its operands, and the normalized hidden states and the pick keys in the
+// handle's workspace.
 constexpr int kHeadMaxRows = 64;
 struct HeadArgs {
     const float * hidden;
@@ -217,7 +217,7 @@ struct HeadArgs {
     float eps;
     const uint16_t * head;
     int64_t head_ld;
-    int rows, d, vocab, max_groups;
+    int rows, d, vocab;
     uint16_t * hn;
     uint64_t * keys;
     int32_t * out_ids;

@@ -37,7 +37,7 @@ def _run(rows, vocab, d, seed, weight=True, nan_row=None, dup=None):
     return hidden, w, head, ids.cpu().numpy(), mx.cpu().numpy()
 
 
-@pytest.mark.parametrize("rows,vocab,d", [(1, 151936, 1024), (7, 1000, 64), (32, 4096, 2048), (33, 5003, 512),
+@pytest.mark.parametrize("rows,vocab,d", [(1, 151936, 1024), (7, 1000, 64), (32, 4096, 2048), (33, 5003, 576),
                                           (64, 151936, 1024)])
 def test_head_pick_matches_the_oracle(rows, vocab, d):
     print("head", rows, vocab, d, flush=True)
