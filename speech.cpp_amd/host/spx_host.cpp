@@ -279,6 +279,123 @@ std::vector<bool> Generation::banned(int vocab, int32_t end_of_speech, int frame
 }
 
 // The chain's device buffers: the sampler, the codes (streams x (picks + 1)), the numbers, the settings, the statuses.
+// ---- haru::Dry and shape_logits over the device entries ----
+
+namespace haru {
+
+struct Dry::Device {
+    int32_t * hist = nullptr;  // size_ ids, then the length, then the update's token
+    float * row = nullptr;     // a logits row (shape_logits, the penalties' read-back)
+    int row_cap = 0;
+    int32_t * pen_tokens = nullptr;
+    double * pen = nullptr;
+    int32_t * npen = nullptr;
+    float * silent = nullptr;
+    uint8_t * speak = nullptr;
+};
+
+namespace {
+spx_dry_config dry_config(const DryConfig & c) {
+    spx_dry_config k{};
+    k.multiplier = c.multiplier;
+    k.base = c.base;
+    k.max_penalty = c.max_penalty;
+    k.allowed_length = c.allowed_length;
+    k.lookback = c.lookback;
+    k.max_match_length = c.max_match_length;
+    return k;
+}
+}  // namespace
+
+Dry::Dry(const DryConfig & config, std::vector<int32_t> exempt)
+    : config_(config), exempt_(std::move(exempt)), d_(new Device()) {
+    if (config.lookback < 0 || config.max_match_length < 0) throw std::invalid_argument("negative DRY lookback or match length");
+    size_ = config.lookback + config.max_match_length + 1;
+    const size_t bytes = (size_t) (size_ + 2) * 4 + (size_t) size_ * 12 + 8 + 16;
+    check_hip(hipMalloc((void **) &d_->hist, bytes), "hipMalloc");
+    d_->pen_tokens = d_->hist + size_ + 2;
+    d_->pen = (double *) (((uintptr_t) (d_->pen_tokens + size_) + 7) & ~(uintptr_t) 7);
+    d_->npen = (int32_t *) (d_->pen + size_);
+    d_->silent = (float *) (d_->npen + 1);
+    d_->speak = (uint8_t *) (d_->silent + 2);
+    check_hip(hipMemset(d_->hist, 0, (size_t) (size_ + 2) * 4), "hipMemset");
+}
+
+Dry::~Dry() {
+    if (d_->hist) (void) hipFree(d_->hist);
+    if (d_->row) (void) hipFree(d_->row);
+    delete d_;
+}
+
+void Dry::update(int32_t token) {
+    int32_t * tok = d_->hist + size_ + 1;
+    check_hip(hipMemcpy(tok, &token, 4, hipMemcpyHostToDevice), "copy token");
+    const spx_dry_config c = dry_config(config_);
+    check_spx(spx_dry_update_rows(1, &c, exempt_.data(), (int) exempt_.size(), tok, d_->hist, d_->hist + size_,
+                                  size_, nullptr));
+    check_hip(hipDeviceSynchronize(), "dry update");
+    if (std::find(exempt_.begin(), exempt_.end(), token) == exempt_.end()) top_id_ = std::max(top_id_, token);
+    fresh_ = true;
+}
+
+const std::vector<std::pair<int32_t, double>> & Dry::penalties() const {
+    if (!fresh_) return penalties_;
+    // a row spanning every token the history holds; its logits are not read back
+    const int vocab = std::max(top_id_ + 1, 1);
+    if (d_->row_cap < vocab) {
+        if (d_->row) (void) hipFree(d_->row);
+        d_->row = nullptr;
+        check_hip(hipMalloc((void **) &d_->row, (size_t) vocab * 4), "hipMalloc");
+        d_->row_cap = vocab;
+    }
+    const float zero[2] = {0.0f, 0.0f};
+    check_hip(hipMemcpy(d_->silent, zero, 8, hipMemcpyHostToDevice), "copy silent");
+    const spx_dry_config c = dry_config(config_);
+    check_spx(spx_haru_shape_rows(d_->row, 1, vocab, vocab, &c, exempt_.data(), (int) exempt_.size(), d_->hist,
+                                  d_->hist + size_, size_, d_->silent, 0, 0, 0, 0.0f, nullptr, d_->pen_tokens, d_->pen,
+                                  d_->npen, size_, nullptr));
+    int32_t n = 0;
+    check_hip(hipMemcpy(&n, d_->npen, 4, hipMemcpyDeviceToHost), "copy count");
+    n = std::min(n, size_);
+    std::vector<int32_t> t((size_t) n);
+    std::vector<double> w((size_t) n);
+    if (n) {
+        check_hip(hipMemcpy(t.data(), d_->pen_tokens, (size_t) n * 4, hipMemcpyDeviceToHost), "copy penalties");
+        check_hip(hipMemcpy(w.data(), d_->pen, (size_t) n * 8, hipMemcpyDeviceToHost), "copy penalties");
+    }
+    penalties_.clear();
+    for (int i = 0; i < n; i++) penalties_.emplace_back(t[(size_t) i], w[(size_t) i]);
+    fresh_ = false;
+    return penalties_;
+}
+
+void Dry::apply(std::vector<float> & logits) const {
+    for (const auto & [t, penalty] : penalties()) logits[(size_t) t] -= (float) penalty;
+}
+
+void shape_logits(std::vector<float> & logits, const Dry & dry, const float silent[2], const TextIds & ids,
+                  float eop_bias, bool must_speak) {
+    const int vocab = (int) logits.size();
+    Dry::Device & d = *dry.d_;
+    if (d.row_cap < vocab) {
+        if (d.row) (void) hipFree(d.row);
+        d.row = nullptr;
+        check_hip(hipMalloc((void **) &d.row, (size_t) vocab * 4), "hipMalloc");
+        d.row_cap = vocab;
+    }
+    const uint8_t speak = must_speak ? 1 : 0;
+    check_hip(hipMemcpy(d.row, logits.data(), (size_t) vocab * 4, hipMemcpyHostToDevice), "copy logits");
+    check_hip(hipMemcpy(d.silent, silent, 8, hipMemcpyHostToDevice), "copy silent");
+    check_hip(hipMemcpy(d.speak, &speak, 1, hipMemcpyHostToDevice), "copy must_speak");
+    const spx_dry_config c = dry_config(dry.config_);
+    check_spx(spx_haru_shape_rows(d.row, 1, vocab, vocab, &c, dry.exempt_.data(), (int) dry.exempt_.size(), d.hist,
+                                  d.hist + dry.size_, dry.size_, d.silent, ids.pad, ids.eop, ids.eos, eop_bias, d.speak,
+                                  nullptr, nullptr, nullptr, 0, nullptr));
+    check_hip(hipMemcpy(logits.data(), d.row, (size_t) vocab * 4, hipMemcpyDeviceToHost), "copy logits");
+}
+
+}  // namespace haru
+
 struct GraphSampler::Device {
     spx_sampler * handle = nullptr;
     void * base = nullptr;
@@ -578,6 +695,49 @@ int spx_host_frame_main(const float * logits, int vocab, const spx_row_params * 
                                                std::vector<int32_t>(token_ids, token_ids + vocab));
         *out_id = f.main(std::vector<float>(logits, logits + vocab),
                          std::vector<int32_t>(history, history + (history ? n_history : 0)), first, again);
+    });
+}
+
+// Haru's Dry over `n` tokens, then its penalties (by rising token, the first `cap`); returns their count in *n_out.
+int spx_host_dry_penalties(const double * cfg3, const int32_t * cfg_ints, const int32_t * exempt, int n_exempt,
+                           const int32_t * tokens, int n, int32_t * out_tokens, double * out_pen, int cap, int * n_out,
+                           char * message, int message_cap) {
+    return report(message, message_cap, [&] {
+        spx_host::haru::DryConfig c;
+        c.multiplier = cfg3[0];
+        c.base = cfg3[1];
+        c.max_penalty = cfg3[2];
+        c.allowed_length = cfg_ints[0];
+        c.lookback = cfg_ints[1];
+        c.max_match_length = cfg_ints[2];
+        spx_host::haru::Dry dry(c, std::vector<int32_t>(exempt, exempt + n_exempt));
+        for (int i = 0; i < n; i++) dry.update(tokens[i]);
+        const auto & p = dry.penalties();
+        *n_out = (int) p.size();
+        for (int i = 0; i < (int) p.size() && i < cap; i++) {
+            out_tokens[i] = p[(size_t) i].first;
+            out_pen[i] = p[(size_t) i].second;
+        }
+    });
+}
+
+// shape_logits of one row after Dry over `n` tokens, in place.
+int spx_host_haru_shape(const double * cfg3, const int32_t * cfg_ints, const int32_t * exempt, int n_exempt,
+                        const int32_t * tokens, int n, float * logits, int vocab, const float * silent, int32_t pad,
+                        int32_t eop, int32_t eos, float eop_bias, int must_speak, char * message, int message_cap) {
+    return report(message, message_cap, [&] {
+        spx_host::haru::DryConfig c;
+        c.multiplier = cfg3[0];
+        c.base = cfg3[1];
+        c.max_penalty = cfg3[2];
+        c.allowed_length = cfg_ints[0];
+        c.lookback = cfg_ints[1];
+        c.max_match_length = cfg_ints[2];
+        spx_host::haru::Dry dry(c, std::vector<int32_t>(exempt, exempt + n_exempt));
+        for (int i = 0; i < n; i++) dry.update(tokens[i]);
+        std::vector<float> l(logits, logits + vocab);
+        spx_host::haru::shape_logits(l, dry, silent, spx_host::haru::TextIds{pad, eop, eos}, eop_bias, must_speak != 0);
+        std::copy(l.begin(), l.end(), logits);
     });
 }
 

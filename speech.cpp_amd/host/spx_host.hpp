@@ -131,6 +131,48 @@ struct Sampling {
 };
 Candidates candidates(const std::vector<float> & logits, const Sampling & s);
 int32_t draw(const std::vector<float> & logits, const Sampling & s, double u);
+
+/** src/families/haru/sampler.h:35-38 */
+struct DryConfig {
+    double multiplier = 0, base = 0, max_penalty = 0;
+    int allowed_length = 0, lookback = 0, max_match_length = 0;
+};
+
+/** src/families/haru/sampler.h:43-46 */
+struct TextIds {
+    int32_t pad = 0, eop = 0, eos = 0;
+};
+
+/**
+ * The DRY state of one text stream (src/families/haru/sampler.h:55-75), kept on the device: update() appends there,
+ * penalties() reads back the list the device forms from it, apply() subtracts them as the reference does.
+ */
+class Dry {
+public:
+    Dry(const DryConfig & config, std::vector<int32_t> exempt);
+    ~Dry();
+    Dry(const Dry &) = delete;
+    Dry & operator=(const Dry &) = delete;
+    void update(int32_t token);
+    const std::vector<std::pair<int32_t, double>> & penalties() const;
+    void apply(std::vector<float> & logits) const;
+
+private:
+    friend void shape_logits(std::vector<float> & logits, const Dry & dry, const float silent[2], const TextIds & ids,
+                             float eop_bias, bool must_speak);
+    DryConfig config_;
+    std::vector<int32_t> exempt_;
+    int size_ = 0;
+    int32_t top_id_ = 0;  // the largest token appended (the penalties' read-back row spans it)
+    struct Device;
+    Device * d_;
+    mutable std::vector<std::pair<int32_t, double>> penalties_;
+    mutable bool fresh_ = true;
+};
+
+/** src/families/haru/sampler.cpp:116-124, on the device with the stream's DRY state. */
+void shape_logits(std::vector<float> & logits, const Dry & dry, const float silent[2], const TextIds & ids,
+                  float eop_bias, bool must_speak);
 }  // namespace haru
 
 namespace drama3 {

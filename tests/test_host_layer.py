@@ -276,3 +276,43 @@ def test_graph_sampler_chain_is_the_oracles():
             st, toks, wts = oracle_lib.tf_candidates(logits[i, r], p, got[r, :i], None)
             assert st == 0
             assert got[r, i] == toks[oracle_lib.pick(wts, u[r * picks + i])], (r, i)
+
+
+@pytest.mark.gpu
+def test_haru_dry_and_shape_logits_are_the_oracles():
+    # haru::Dry (src/families/haru/sampler.cpp:87-114) and shape_logits (:116-124) of the host layer, their state on the
+    # device, against the oracle: the penalties after each prefix of a sequence, and the shaped logits, bit for bit.
+    spx = workloads.spx_module()
+    lib = host()
+    vp, i32 = ctypes.c_void_p, ctypes.c_int
+    lib.spx_host_dry_penalties.argtypes = [vp, vp, vp, i32, vp, i32, vp, vp, i32, vp, ctypes.c_char_p, i32]
+    lib.spx_host_dry_penalties.restype = i32
+    lib.spx_host_haru_shape.argtypes = [vp, vp, vp, i32, vp, i32, vp, i32, vp, i32, i32, i32, ctypes.c_float, i32,
+                                        ctypes.c_char_p, i32]
+    lib.spx_host_haru_shape.restype = i32
+    ptr = lambda a: a.ctypes.data_as(ctypes.c_void_p)
+    rng = np.random.default_rng(71)
+    vocab, pad, eop, eos = 512, 509, 510, 511
+    exempt = np.array([pad, eop, eos], dtype=np.int32)
+    for allowed, lookback, max_match in ((2, 32, 6), (1, 8, 3)):
+        config = spx.DryConfig(0.8, 1.75, 3.0, allowed, lookback, max_match, 0)
+        cfg3 = np.array([0.8, 1.75, 3.0])
+        cfgi = np.array([allowed, lookback, max_match], dtype=np.int32)
+        seq = rng.choice(np.r_[np.arange(6), exempt], 60).astype(np.int32)
+        for n in (0, 5, 17, 40, 60):
+            cap = lookback + max_match + 1
+            toks, pens, nout = np.zeros(cap, np.int32), np.zeros(cap), ctypes.c_int()
+            msg = ctypes.create_string_buffer(256)
+            assert lib.spx_host_dry_penalties(ptr(cfg3), ptr(cfgi), ptr(exempt), 3, ptr(seq), n, ptr(toks), ptr(pens),
+                                              cap, ctypes.byref(nout), msg, 256) == 0, msg.value
+            _, ot, op = oracle_lib.dry_run(config, exempt, seq[:n])
+            assert nout.value == len(ot)
+            np.testing.assert_array_equal(toks[:len(ot)], ot)
+            np.testing.assert_array_equal(pens[:len(ot)].view(np.int64), op.view(np.int64))
+            logits = rng.normal(0, 2, vocab).astype(np.float32)
+            silent = rng.normal(0, 2, 2).astype(np.float32)
+            got = logits.copy()
+            assert lib.spx_host_haru_shape(ptr(cfg3), ptr(cfgi), ptr(exempt), 3, ptr(seq), n, ptr(got), vocab,
+                                           ptr(silent), pad, eop, eos, 0.25, n % 2, msg, 256) == 0, msg.value
+            want = oracle_lib.haru_shape(logits, ot, op, silent, pad, eop, eos, 0.25, bool(n % 2))
+            np.testing.assert_array_equal(got.view(np.int32), want.view(np.int32))
