@@ -126,3 +126,31 @@ def test_drama3_main_tokens():
                                           window, None)
         redrawn += int(plain != want)
     assert redrawn > 0  # the rule was exercised
+
+
+@pytest.mark.parametrize("cap", [100, 4096])
+def test_candidate_lists_of_a_mixed_batch(cap):
+    # spx_candidates_rows over rows of the three flavors, top-k on and off, wide and narrow top-p: the first `cap`
+    # candidates of each row in the reference's order with its weights, and the kept count, against the oracle.
+    import torch
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(cap)
+    rows, vocab = 24, 4096
+    logits = rng.normal(0, 2, (rows, vocab)).astype(np.float32)
+    flavor = np.array([0, 1, 2] * (rows // 3), dtype=np.int32)
+    p = spx.row_params(rows, 0, temperature=rng.uniform(0.6, 1.4, rows).astype(np.float32),
+                       top_k=rng.choice([0, 40, 300, 5000], rows), top_p=rng.choice([0.5, 0.9, 1.0], rows).astype(np.float32))
+    p["flavor"] = flavor
+    w = workloads.Workload(name="lists", logits=logits, dtype="f32", params=p, u=np.zeros(rows), hist=None,
+                           hist_off=None, banned=None, banned_stride=0)
+    reports, cids, cw = oracle_lib.sample_rows(w, cap=cap)
+    s = spx.Sampler(max_rows=rows, max_vocab=vocab, max_hist=0, max_out=0)
+    toks, wts, n, status = s.candidates_rows(torch.from_numpy(logits).cuda(), spx.device_params(p), cap)
+    torch.cuda.synchronize()
+    toks, wts, n, status = toks.cpu().numpy(), wts.cpu().numpy(), n.cpu().numpy(), status.cpu().numpy()
+    for r in range(rows):
+        assert status[r] == reports[r]["status"] == 0, r
+        assert n[r] == reports[r]["kept"], (r, n[r], reports[r]["kept"])
+        m = min(cap, int(n[r]))
+        why = gpu_harness._check_candidates(w, r, toks[r, :m], wts[r, :m], cids[r, :m], cw[r, :m], flavor[r] == 0, None)
+        assert why is None, (r, why)
