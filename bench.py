@@ -31,6 +31,7 @@ sys.path.insert(0, os.path.join(ROOT, "tests"))
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E
 WORKLOAD_LABELS = {
     "haru": "Haru-4B-style text sampling: 256 x 151936 fp32, hist 1024, rep 1.1 + presence 0.5, T 0.7, top-p 0.9 (transformers rules, which take the penalties)",
+    "haru-flavor": "Haru's own rules at its defaults: 256 x 151936 fp32, T 0.7, top-k 25, top-p 1, float32 softmax",
     "asr": "Qwen3-ASR-style greedy: 64 x 151936 fp32, 300 banned ids, argmax (spx_argmax_rows)",
     "mixed": "heterogeneous mixed batch: 2048 x 151936 bf16, per-row T/top-k/top-p, hist U[0,2048], 1% greedy",
     "predictor": "Qwen3-TTS code-predictor batch: 480 x 2048 fp32, hist 64, rep 1.05, T 0.9, top-k 50",

@@ -169,6 +169,14 @@ def make(name, rows=None, seed=1234):
         params = spx.row_params(rows, spx.TRANSFORMERS, temperature=0.7, top_k=0, top_p=0.9, repetition_penalty=1.1,
                                 presence_penalty=0.5)
         dtype = "f32"
+    elif name == "haru-flavor":
+        # Haru's own rules at its file's defaults (haru::Sampling: T 0.7, top-k 25, top-p 1), no penalties (its DRY
+        # shapes the logits before the draw)
+        rows = rows or 256
+        vocab = 151936
+        logits = zipf_logits(rng, rows, vocab)
+        params = spx.row_params(rows, spx.HARU, temperature=0.7, top_k=25, top_p=1.0)
+        dtype = "f32"
     elif name == "mixed":
         rows = rows or 2048
         vocab = 151936
