@@ -74,7 +74,7 @@ hipError_t launch_sampler(const spx::Launch & a, hipStream_t s) {
 // The resolving kernel after a sampling launch: `grid` work-groups take the rows the sampling kernel left, if any.
 hipError_t launch_resolver(const spx::Launch & r, int grid, hipStream_t s) {
     using namespace spx;
-    if (r.block == kBlockResolve) return r.dtype == SPX_BF16 ? resolve_bf16_1024(r, grid, s) : resolve_f32_1024(r, grid, s);
+    if (r.block != kBlockSmall) return r.dtype == SPX_BF16 ? resolve_bf16_1024(r, grid, s) : resolve_f32_1024(r, grid, s);
     return r.dtype == SPX_BF16 ? resolve_bf16_256(r, grid, s) : resolve_f32_256(r, grid, s);
 }
 

@@ -12,8 +12,11 @@ namespace spx {
 // 256 below.
 constexpr int kBlockBig = 1024;
 constexpr int kBlockSmall = 256;
-// Threads per work-group of the resolving kernel for large vocabularies (256 below): up to 256 VGPRs per lane.
-constexpr int kBlockResolve = 512;
+// Threads per work-group of the resolving kernel for large vocabularies (256 below): 1024 (16 waves a CU to hide the
+// latency of each token's work; 128 VGPRs a lane), or 512 with the smaller wide-path layout where the 1024-thread
+// one's LDS does not fit beside a long history list.
+constexpr int kBlockResolve = 1024;
+constexpr int kBlockResolveNarrow = 512;
 constexpr int kBigVocab = 16384;
 // Final logits each lane holds per step of the stream (four 16-byte vectors of fp32, two of bf16).
 constexpr int kE = 16;
@@ -28,13 +31,14 @@ constexpr int kMaxSplitsGreedy = 16;
 // LDS bytes of a chunk's control block (its counters, bins and first-step bounds).
 constexpr int kCtlBytes = 2048;
 // The wide path's LDS (rows whose draw runs past the candidates held): NB bins of the row's quotients and room for CAP
-// gathered tokens, per work-group size.
+// gathered tokens, per work-group size. A bin holding more than CAP tokens takes a finer histogram and more reads, so
+// the 1024-thread layout, with most of a CU's LDS, gathers twice as many.
 template <int B>
 struct WideDims;
 template <>
 struct WideDims<1024> {
     static constexpr int NB = 2048;
-    static constexpr int CAP = 2048;
+    static constexpr int CAP = 4096;
 };
 template <>
 struct WideDims<512> {

@@ -3229,15 +3229,31 @@ __global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
         return hipGetLastError();                                                                               \
     }                                                                                                           \
     hipError_t resolve_##NAME(const Launch & a, int grid, hipStream_t s) {                                       \
-        constexpr int RB = B == kBlockBig ? kBlockResolve : B;                                                  \
-        hipLaunchKernelGGL((resolve_kernel<T, RB>), dim3(grid), dim3(RB), a.lds_bytes, s, a);                   \
+        if constexpr (B == kBlockBig) {                                                                         \
+            if (a.block == kBlockResolveNarrow)                                                                 \
+                hipLaunchKernelGGL((resolve_kernel<T, kBlockResolveNarrow>), dim3(grid), dim3(kBlockResolveNarrow), \
+                                   a.lds_bytes, s, a);                                                          \
+            else                                                                                                \
+                hipLaunchKernelGGL((resolve_kernel<T, kBlockResolve>), dim3(grid), dim3(kBlockResolve),         \
+                                   a.lds_bytes, s, a);                                                          \
+        } else {                                                                                                \
+            hipLaunchKernelGGL((resolve_kernel<T, B>), dim3(grid), dim3(B), a.lds_bytes, s, a);                 \
+        }                                                                                                       \
         return hipGetLastError();                                                                               \
     }                                                                                                           \
     hipError_t lds_limit_##NAME(int bytes) {                                                                    \
         hipError_t e = hipFuncSetAttribute((const void *) sampler_kernel<T, B>,                                 \
                                            hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                  \
         if (e != hipSuccess) return e;                                                                          \
-        return hipFuncSetAttribute((const void *) resolve_kernel<T, B == kBlockBig ? kBlockResolve : B>,        \
-                                   hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                          \
+        if constexpr (B == kBlockBig) {                                                                         \
+            e = hipFuncSetAttribute((const void *) resolve_kernel<T, kBlockResolveNarrow>,                      \
+                                    hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                         \
+            if (e != hipSuccess) return e;                                                                      \
+            return hipFuncSetAttribute((const void *) resolve_kernel<T, kBlockResolve>,                         \
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                      \
+        } else {                                                                                                \
+            return hipFuncSetAttribute((const void *) resolve_kernel<T, B>,                                     \
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                      \
+        }                                                                                                       \
     }                                                                                                           \
     }

@@ -41,9 +41,16 @@ inline size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, 
     return off;
 }
 
+// The wide path's LDS bytes for a resolving work-group of `block` threads.
+inline size_t wide_bytes_of(int block) {
+    return block == kBlockResolve ? wide_lds_bytes<kBlockResolve>()
+         : block == kBlockResolveNarrow ? wide_lds_bytes<kBlockResolveNarrow>() : wide_lds_bytes<kBlockSmall>();
+}
+
 // The resolving kernel's launch record from the sampling one: a whole row per work-group (its special tokens over the
-// whole vocabulary), 1024 threads for large vocabularies, and an LDS layout whose last region is the wide path's (the
-// radix path's 2 x kKeep listed entries and its histograms fit there too).
+// whole vocabulary), 1024 threads for large vocabularies (512 where a long history list leaves too little LDS for the
+// 1024-thread wide path), and an LDS layout whose last region is the wide path's (the radix path's 2 x kKeep listed
+// entries and its histograms fit there too).
 inline size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist) {
     r = a;
     r.block = a.vocab >= kBigVocab ? kBlockResolve : kBlockSmall;
@@ -64,10 +71,13 @@ inline size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist)
     off = align_up(off, 16);
     r.off_cand = (int) off;
     r.off_sort = (int) (off + 2 * kKeep * 8);
-    const size_t wide = r.block == kBlockResolve ? wide_lds_bytes<kBlockResolve>() : wide_lds_bytes<kBlockSmall>();
-    off = std::max((size_t) r.off_sort + 3 * 1024, off + wide);
-    r.lds_bytes = (int) off;
-    return off;
+    size_t end = std::max((size_t) r.off_sort + 3 * 1024, off + wide_bytes_of(r.block));
+    if (r.block == kBlockResolve && end > kLdsMax) {
+        r.block = kBlockResolveNarrow;
+        end = std::max((size_t) r.off_sort + 3 * 1024, off + wide_bytes_of(r.block));
+    }
+    r.lds_bytes = (int) end;
+    return end;
 }
 
 // Chunks per row: about one work-group of 1024 threads, or four of 256, per CU (`cus` of them); chunks of at least

@@ -67,7 +67,11 @@ static void check(int cus, int max_rows, int rows, int vocab, int max_hist, bool
         REQUIRE((size_t) r.lds_bytes <= limit, f, ARGS);
         REQUIRE((size_t) r.off_own >= r.off_spec + (size_t) (vocab + 31) / 32 * 4, f, ARGS);
         REQUIRE((size_t) r.off_cand >= (size_t) r.off_own + (size_t) r.own_cap * 4, f, ARGS);
-        const size_t wide = r.block == kBlockResolve ? wide_lds_bytes<kBlockResolve>() : wide_lds_bytes<kBlockSmall>();
+        const size_t wide = wide_bytes_of(r.block);
+        REQUIRE(vocab >= kBigVocab ? r.block == kBlockResolve || r.block == kBlockResolveNarrow : r.block == kBlockSmall,
+                f, ARGS);
+        // the 512-thread layout only where the 1024-thread one would not have fit
+        if (r.block == kBlockResolveNarrow) REQUIRE((size_t) r.off_cand + wide_bytes_of(kBlockResolve) > kLdsMax, f, ARGS);
         REQUIRE((size_t) r.off_cand + wide <= (size_t) r.lds_bytes, f, ARGS);
         REQUIRE(r.off_sort >= r.off_cand + 2 * kKeep * 8 && r.off_sort + 3 * 1024 <= r.lds_bytes, f, ARGS);
     }
@@ -75,6 +79,21 @@ static void check(int cus, int max_rows, int rows, int vocab, int max_hist, bool
 }
 
 int main() {
+    // handles create accepts: every history up to 16384 ids at the 151936-token vocabulary (the resolving kernel's
+    // narrower layout where the 1024-thread one does not fit), and the 1024-thread layout up to 8192 ids
+    for (int max_hist : {0, 2048, 8192, 16384}) {
+        if (lds_bound(151936, max_hist) > kLdsMax) {
+            fails++;
+            std::printf("refused: vocab 151936 max_hist %d\n", max_hist);
+        }
+        Launch a{}, r{};
+        a.vocab = 151936;
+        plan_resolve(r, a, max_hist);
+        if ((max_hist <= 8192) != (r.block == kBlockResolve)) {
+            fails++;
+            std::printf("resolving block %d at max_hist %d\n", r.block, max_hist);
+        }
+    }
     const int cus_list[] = {256, 80, 304, 1};
     const int rows_list[] = {1, 2, 3, 4, 7, 16, 63, 64, 65, 85, 128, 255, 256, 257, 341, 480, 512, 1000, 1024, 2048, 4096};
     const int vocab_list[] = {1, 2, 31, 63, 64, 65, 100, 1000, 2048, 3072, 4096, 4097, 12288, 15000, 16000, 16383,

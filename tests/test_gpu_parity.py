@@ -374,20 +374,23 @@ def test_transformers_top_p_over_the_top_k_and_fish_floor_on_the_device(sampler)
             check(sampler, w, allow_explained=False)
 
 
-def test_long_histories(sampler):
-    # Histories of 8192 ids (the talker's grows one id per frame without a bound), with repetition, presence and
-    # frequency penalties, on both work-group sizes.
+@pytest.mark.parametrize("n_hist", [8192, 16384])
+def test_long_histories(sampler, n_hist):
+    # Histories of 8192 and 16384 ids (the talker's grows one id per frame without a bound), with repetition, presence
+    # and frequency penalties, on both work-group sizes; at 16384 ids the resolving kernel takes its 512-thread layout.
     spx = workloads.spx_module()
-    big = spx.Sampler(max_rows=8, max_vocab=151936, max_hist=8192, max_out=MAX_OUT)
+    big = spx.Sampler(max_rows=8, max_vocab=151936, max_hist=n_hist, max_out=MAX_OUT)
     rng = np.random.default_rng(29)
     for vocab in (151936, 3072):
         rows = 4
         logits = workloads.zipf_logits(rng, rows, vocab)
-        hists = [np.concatenate([np.argsort(-logits[r])[:100].repeat(8), rng.integers(0, vocab, 7392)]) for r in range(rows)]
+        logits[2] = rng.normal(0, 1, vocab)  # a flat row: its top-p set is wider than the sampling kernel holds
+        hists = [np.concatenate([np.argsort(-logits[r])[:100].repeat(8), rng.integers(0, vocab, n_hist - 800)])
+                 for r in range(rows)]
         hist, off = workloads.csr(hists)
         p = spx.row_params(rows, temperature=0.8, top_k=np.array([0, 50, 0, 300]), top_p=0.9,
                            repetition_penalty=1.1, presence_penalty=0.3,
                            frequency_penalty=np.array([0.0, 0.05, 0.1, 0.0], dtype=np.float32))
-        w = workloads.Workload(name=f"hist 8192 x {vocab}", logits=logits, dtype="f32", params=p,
+        w = workloads.Workload(name=f"hist {n_hist} x {vocab}", logits=logits, dtype="f32", params=p,
                                u=workloads.uniforms(31, rows), hist=hist, hist_off=off, banned=None, banned_stride=0)
         check(big, w)
