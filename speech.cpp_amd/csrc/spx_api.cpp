@@ -68,6 +68,7 @@ hipError_t launch_sampler(const spx::Launch & a, hipStream_t s) {
     using namespace spx;
     if (a.nwg == 0) return hipSuccess;
     if (a.block == kBlockBig) return a.dtype == SPX_BF16 ? launch_bf16_1024(a, s) : launch_f32_1024(a, s);
+    if (a.block == kBlockMid) return a.dtype == SPX_BF16 ? launch_bf16_512(a, s) : launch_f32_512(a, s);
     return a.dtype == SPX_BF16 ? launch_bf16_256(a, s) : launch_f32_256(a, s);
 }
 
@@ -82,7 +83,8 @@ hipError_t launch_resolver(const spx::Launch & r, int grid, hipStream_t s) {
 hipError_t set_lds_limits(int bytes) {
     using namespace spx;
     if (bytes <= 65536) return hipSuccess;
-    for (auto f : {lds_limit_f32_1024, lds_limit_bf16_1024, lds_limit_f32_256, lds_limit_bf16_256}) {
+    for (auto f : {lds_limit_f32_1024, lds_limit_bf16_1024, lds_limit_f32_512, lds_limit_bf16_512, lds_limit_f32_256,
+                   lds_limit_bf16_256}) {
         const hipError_t e = f(bytes);
         if (e != hipSuccess) return e;
     }

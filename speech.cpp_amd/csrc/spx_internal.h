@@ -8,9 +8,11 @@
 
 namespace spx {
 
-// Threads per work-group: 1024 for rows of at least kBigVocab tokens (one work-group per CU streams a whole row),
-// 256 below.
+// Threads per work-group: 1024 for rows of at least kBigVocab tokens (one work-group per CU streams a whole row), 512
+// for such rows in batches of at least two rows per CU (two work-groups per CU, one row's fixed phases under the other's
+// stream), 256 below.
 constexpr int kBlockBig = 1024;
+constexpr int kBlockMid = 512;
 constexpr int kBlockSmall = 256;
 // Threads per work-group of the resolving kernel for large vocabularies (256 below): 1024 (16 waves a CU to hide the
 // latency of each token's work; 128 VGPRs a lane), or 512 with the smaller wide-path layout where the 1024-thread
@@ -163,11 +165,13 @@ constexpr int kMaxDevices = 64;
 #include <hip/hip_runtime.h>
 
 namespace spx {
-// The kernels' variants (spx_k_*.hip): logits of fp32 or bf16, work-groups of 1024 or 256 threads. Each variant has
-// the one-pass sampling kernel (launch_*) and the kernel that resolves the rows it leaves (resolve_*); lds_limit_*
-// lets both take `bytes` of dynamic LDS.
+// The kernels' variants (spx_k_*.hip): logits of fp32 or bf16, work-groups of 1024, 512 or 256 threads. Each
+// variant has the one-pass sampling kernel (launch_*) and, but for the 512-thread ones, the kernel that resolves the
+// rows it leaves (resolve_*); lds_limit_* lets them take `bytes` of dynamic LDS.
 hipError_t launch_f32_1024(const Launch & a, hipStream_t s);
 hipError_t launch_bf16_1024(const Launch & a, hipStream_t s);
+hipError_t launch_f32_512(const Launch & a, hipStream_t s);
+hipError_t launch_bf16_512(const Launch & a, hipStream_t s);
 hipError_t launch_f32_256(const Launch & a, hipStream_t s);
 hipError_t launch_bf16_256(const Launch & a, hipStream_t s);
 hipError_t resolve_f32_1024(const Launch & a, int grid, hipStream_t s);
@@ -240,6 +244,8 @@ hipError_t launch_head_pick(const HeadArgs & h, hipStream_t s);
 hipError_t launch_haru_shape(const DryArgs & d, hipStream_t s);
 hipError_t lds_limit_f32_1024(int bytes);
 hipError_t lds_limit_bf16_1024(int bytes);
+hipError_t lds_limit_f32_512(int bytes);
+hipError_t lds_limit_bf16_512(int bytes);
 hipError_t lds_limit_f32_256(int bytes);
 hipError_t lds_limit_bf16_256(int bytes);
 }  // namespace spx

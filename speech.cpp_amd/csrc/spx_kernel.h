@@ -3220,6 +3220,20 @@ __global__ __launch_bounds__(B, 1) void resolve_kernel(Launch a) {
 
 }  // namespace spx
 
+// A variant of the sampling kernel alone (its rows resolved by another variant's resolving kernel): the launcher
+// spx::launch_<NAME> and its LDS limit spx::lds_limit_<NAME>.
+#define SPX_SAMPLER_VARIANT(T, B, NAME)                                                                         \
+    namespace spx {                                                                                             \
+    hipError_t launch_##NAME(const Launch & a, hipStream_t s) {                                                 \
+        hipLaunchKernelGGL((sampler_kernel<T, B>), dim3(a.nwg), dim3(B), a.lds_bytes, s, a);                    \
+        return hipGetLastError();                                                                               \
+    }                                                                                                           \
+    hipError_t lds_limit_##NAME(int bytes) {                                                                    \
+        return hipFuncSetAttribute((const void *) sampler_kernel<T, B>,                                         \
+                                   hipFuncAttributeMaxDynamicSharedMemorySize, bytes);                          \
+    }                                                                                                           \
+    }
+
 // One variant of the kernels: the launchers spx::launch_<NAME> and spx::resolve_<NAME>, and their LDS limit
 // spx::lds_limit_<NAME>.
 #define SPX_KERNEL_VARIANT(T, B, NAME)                                                                          \

@@ -32,7 +32,9 @@ inline size_t plan_lds(spx::Launch & a, int block, int chunk, bool greedy_only, 
     a.own_cap = (int) cap;
     a.off_own = (int) off;
     if (has_hist) off += cap * 4;
-    a.cand_cap = std::max(2 * block, kSortCap);  // also where the merge of a row's chunks sorts up to kSortCap entries
+    // also where the merge of a row's chunks sorts up to kSortCap entries; a 512-thread work-group's first step sees
+    // half the tokens a 1024-thread one's does, so its threshold starts lower and it keeps as many as that one
+    a.cand_cap = block == kBlockMid ? 2 * kBlockBig : std::max(2 * block, kSortCap);
     off = align_up(off, 16);
     a.off_cand = (int) off;
     a.off_sort = (int) (off + (size_t) a.cand_cap * 8);
@@ -84,10 +86,16 @@ inline size_t plan_resolve(spx::Launch & r, const spx::Launch & a, int max_hist)
 // one step of the work-group (kE tokens a lane) and a multiple of 64 tokens, and few enough that the row's last chunk
 // can merge them (kMaxSplits; kMaxSplitsGreedy for argmax-only calls, whose chunks publish no candidates). The
 // workspace holds kMaxSplitsGreedy partials and kMaxSplits x kKeep candidates per row, so no chunk index reaches
-// past its row's share.
+// past its row's share. Large rows in batches of two or more per CU take 512-thread work-groups, a whole row each,
+// where two of them fit a CU's LDS.
 inline void plan_rows(Launch & a, int cus, int max_hist, bool greedy_only, bool has_hist, bool has_ban) {
-    const int block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
-    const int per_cu = block == kBlockBig ? 1 : 4;
+    int block = a.vocab >= kBigVocab ? kBlockBig : kBlockSmall;
+    if (block == kBlockBig && a.rows >= 2 * cus) {
+        Launch probe = a;
+        if (plan_lds(probe, kBlockMid, a.vocab, greedy_only, has_hist, has_ban, max_hist) <= kLdsMax / 2)
+            block = kBlockMid;
+    }
+    const int per_cu = block == kBlockBig ? 1 : block == kBlockMid ? 2 : 4;
     const int max_splits = greedy_only ? kMaxSplitsGreedy : kMaxSplits;
     int splits = std::max(1, (per_cu * cus + a.rows - 1) / std::max(a.rows, 1));
     splits = std::min(splits, max_splits);
@@ -106,7 +114,7 @@ inline void plan_rows(Launch & a, int cus, int max_hist, bool greedy_only, bool 
 // either work-group size a call may take, and the resolving kernel's.
 inline size_t lds_bound(int max_vocab, int max_hist) {
     size_t lds_max = 0;
-    for (int block : {kBlockBig, kBlockSmall}) {
+    for (int block : {kBlockBig, kBlockMid, kBlockSmall}) {
         Launch probe{};
         lds_max = std::max(lds_max, plan_lds(probe, block, max_vocab, false, max_hist > 0, true, max_hist));
     }

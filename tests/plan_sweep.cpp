@@ -50,6 +50,10 @@ static void check(int cus, int max_rows, int rows, int vocab, int max_hist, bool
     REQUIRE(!has_hist || (size_t) a.off_cand >= (size_t) a.off_own + (size_t) a.own_cap * 4, f, ARGS);
     REQUIRE(a.off_cand % 16 == 0 && a.off_sort >= a.off_cand + a.cand_cap * 8, f, ARGS);
     REQUIRE(a.cand_cap >= 2 * a.block, f, ARGS);
+    // 512-thread work-groups: large rows, two rows or more per CU, a whole row each, two work-groups in a CU's LDS
+    if (a.block == kBlockMid)
+        REQUIRE(vocab >= kBigVocab && rows >= 2 * cus && a.splits == 1 && 2 * (size_t) a.lds_bytes <= kLdsMax, f, ARGS);
+    REQUIRE(a.block == (vocab >= kBigVocab ? (a.block == kBlockMid ? kBlockMid : kBlockBig) : kBlockSmall), f, ARGS);
     if (!greedy_only) {
         REQUIRE(a.off_sort + kSortCap * 8 <= a.lds_bytes, f, ARGS);
         REQUIRE(a.splits * kKeep <= kSortCap && a.splits * kKeep <= a.cand_cap, f, ARGS);  // the merge's entries
