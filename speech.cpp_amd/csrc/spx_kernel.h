@@ -1698,8 +1698,8 @@ __device__ __forceinline__ void set_window(FbRow & r, float top, int b0, int b1)
 
 // Sorts v[0..n) in falling order (bitonic, over the next power of two, padded with 0, below every entry); v holds at
 // least that many. Ends with a barrier.
-template <int B>
-__device__ __forceinline__ void block_sort_desc_u64(uint64_t * v, int n) {
+template <int B, typename K>
+__device__ __forceinline__ void block_sort_desc(K * v, int n) {
     int p = 1;
     while (p < n) p <<= 1;
     for (int i = n + (int) threadIdx.x; i < p; i += B) v[i] = 0ull;
@@ -1710,7 +1710,7 @@ __device__ __forceinline__ void block_sort_desc_u64(uint64_t * v, int n) {
                 const int lo = 2 * i - (i & (stride - 1));
                 const int hi = lo + stride;
                 const bool down = (lo & size) == 0;
-                const uint64_t x = v[lo], y = v[hi];
+                const K x = v[lo], y = v[hi];
                 if ((x < y) == down) {
                     v[lo] = y;
                     v[hi] = x;
@@ -1719,6 +1719,10 @@ __device__ __forceinline__ void block_sort_desc_u64(uint64_t * v, int n) {
         }
     }
     __syncthreads();
+}
+template <int B>
+__device__ __forceinline__ void block_sort_desc_u64(uint64_t * v, int n) {
+    block_sort_desc<B, uint64_t>(v, n);
 }
 
 // Exclusive prefix sum of one 64-bit value per thread over the work-group; `total` gets the sum. red: LDS of B/64.
@@ -1868,6 +1872,45 @@ __device__ __forceinline__ void gather_in_order(FbRow & r, WideMem<NB, CAP> & m,
     __syncthreads();
 }
 
+// The tokens of bin b (a finite bin before the last) when they are a run of one value, at most 2 x CAP of them: their
+// entries' low words (the ids complemented) sorted falling, so ids rising, which is the row's order, in the words at
+// m.ent. Returns the run's key + 1, or 0 when the bin holds more tokens or more than one value.
+template <typename T, int B, int NB, int CAP>
+__device__ __forceinline__ uint64_t gather_run(FbRow & r, WideMem<NB, CAP> & m, float top, int b) {
+    const int tid = threadIdx.x;
+    const uint32_t n = m.pre_cnt[b + 1] - m.pre_cnt[b];
+    if (b >= NB - 1 || n > (uint32_t) (2 * CAP)) return 0;
+    uint32_t * gid = (uint32_t *) m.ent;
+    uint32_t * kr = (uint32_t *) m.wb;  // the bin's smallest and largest key
+    if (tid == 0) {
+        m.n_gath = 0u;
+        kr[0] = ~0u;
+        kr[1] = 0u;
+    }
+    __syncthreads();
+    set_window<NB>(r, top, b, b);
+    uint32_t klo = ~0u, khi = 0u;
+    fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
+        if (!e || banned || !(qq > -INFINITY) || wide_bin<NB>(qq, top) != b) return;
+        const uint32_t at = atomicAdd(&m.n_gath, 1u);
+        if (at < (uint32_t) (2 * CAP)) gid[at] = (uint32_t) e;
+        klo = min(klo, entry_key(e));
+        khi = max(khi, entry_key(e));
+    });
+    r.win = false;
+    if (klo != ~0u) {
+        atomicMin(&kr[0], klo);
+        atomicMax(&kr[1], khi);
+    }
+    __syncthreads();
+    const bool run = m.n_gath == n && kr[0] == kr[1];
+    const uint32_t key = kr[0];
+    __syncthreads();
+    if (!run) return 0;
+    block_sort_desc<B, uint32_t>(gid, (int) n);
+    return (uint64_t) key + 1;
+}
+
 // The last bin of a batch starting at bin b0 whose tokens fit CAP; -1 when bin b0 alone holds more.
 template <int NB, int CAP>
 __device__ __forceinline__ int batch_end(const WideMem<NB, CAP> & m, int b0) {
@@ -1882,8 +1925,9 @@ __device__ __forceinline__ int batch_end(const WideMem<NB, CAP> & m, int b0) {
 // token whose sum before it reaches top_p. Both are taken by one lane over batches of bins gathered in order; the sum
 // stops at the first term below half a unit of it (every later term is smaller and leaves it as it is), the zeroing
 // once the running sum has passed top_p by two units (every later token is zeroed). Where top_p applies this also
-// resolves the row: its pick and its listed candidates. Returns 0: the row is not resolved here (the pick is left to
-// the fixed-point questions), 1: resolved, -1: a bin holds more tokens than a batch takes.
+// resolves the row: its pick and its listed candidates. A bin of more tokens than a batch takes is a batch of its own
+// when it is a run of one value (gather_run). Returns 0: the row is not resolved here (the pick is left to the
+// fixed-point questions), 1: resolved, -1: a bin holds more tokens than a batch takes and is no such run.
 template <typename T, int B, int NB, int CAP>
 __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan & pl, FbRow & r, WideMem<NB, CAP> & m,
                                           float top, uint64_t lowest, float & sum_out) {
@@ -1897,12 +1941,22 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
         int b0 = 0;
         bool stop = false;
         while (!stop && b0 <= NB && m.pre_cnt[b0] < k) {
-            const int b1 = batch_end(m, b0);
-            if (b1 < 0) return -1;
-            gather_in_order<T, B>(r, m, top, b0, b1, ord);
+            // The tokens from bin b0 on weigh at most what its upper edge does (widened past the roundings of the
+            // bins): below half a unit of the sum, the sum is final (the far bin, too large for a batch, among them).
+            if (b0 > 0) {
+                const float qhi = b0 == NB ? -INFINITY
+                                           : top - (float) b0 / kWideScale + (__builtin_fabsf(top) + 1.0f) * (1.0f / 65536.0f);
+                if (haru_exp(qhi, top) < half_ulp(sumf)) break;
+            }
+            int b1 = batch_end(m, b0);
+            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0) : 0;
+            if (b1 < 0 && !runk) return -1;
+            if (runk) b1 = b0;
+            else gather_in_order<T, B>(r, m, top, b0, b1, ord);
             if (tid == 0) {
                 const uint32_t base = m.pre_cnt[b0];
                 const int n = (int) (m.pre_cnt[b1 + 1] - base);
+                const float erun = runk ? haru_exp(key_float((uint32_t) (runk - 1)), top) : 0.0f;
                 float s = sumf;
                 bool st = false;
                 for (int i = 0; i < n && !st; i++) {
@@ -1910,7 +1964,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                         st = true;
                         break;
                     }
-                    const float e = haru_exp(entry_value(ord[i]), top);
+                    const float e = runk ? erun : haru_exp(entry_value(ord[i]), top);
                     if (e < half_ulp(s)) st = true;
                     else s += e;
                 }
@@ -1949,12 +2003,18 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
         int b0 = 0;
         bool stop = false;
         while (!stop && b0 <= NB && m.pre_cnt[b0] < k) {
-            const int b1 = batch_end(m, b0);
-            if (b1 < 0) return -1;
-            gather_in_order<T, B>(r, m, top, b0, b1, ord);
+            int b1 = batch_end(m, b0);
+            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0) : 0;
+            if (b1 < 0 && !runk) return -1;
+            if (runk) b1 = b0;
+            else gather_in_order<T, B>(r, m, top, b0, b1, ord);
             const uint32_t base = m.pre_cnt[b0];
             const int n = (int) (m.pre_cnt[b1 + 1] - base);
             if (tid == 0) {
+                // the batch's entry at place i: a run's from its sorted ids
+                const uint32_t * gid = (const uint32_t *) m.ent;
+                auto at = [&](int i) { return runk ? ((runk - 1) << 32) | (uint64_t) gid[i] : ord[i]; };
+                const float erun = runk ? haru_exp(key_float((uint32_t) (runk - 1)), top) : 0.0f;
                 float cum = sh[0];
                 bool st = false;
                 double total = dsh[0], share = dsh[1];
@@ -1964,7 +2024,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                         st = true;
                         break;
                     }
-                    const float e = haru_exp(entry_value(ord[i]), top);
+                    const float e = runk ? erun : haru_exp(entry_value(ord[i]), top);
                     const float pr = e / sumf;
                     const float c = cum + pr;
                     const bool zero = !(c - pr < tp);
@@ -1973,7 +2033,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                     if (sweep == 0) {
                         total += w;
                         if (rank < (uint64_t) nl) {
-                            a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(ord[i]);
+                            a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(at(i));
                             a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = w;
                         }
                         if (zero && cum >= stop_at && rank + 1 >= (uint64_t) nl) st = true;
@@ -1982,7 +2042,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                         share += w / total;
                         if (rank + 1 < k && share > u) {
                             ush[0] = 1;
-                            ush[1] = ord[i];
+                            ush[1] = at(i);
                             st = true;
                         } else if (zero && cum >= stop_at) {
                             st = true;  // every later weight is 0: the share rises no more
@@ -2012,9 +2072,14 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
         pick = lowest;
     } else if (!pick) {
         const int b = bin_of_rank<NB>(m.pre_cnt, k - 1);
-        if (m.pre_cnt[b + 1] - m.pre_cnt[b] > (uint32_t) CAP) return -1;
-        gather_in_order<T, B>(r, m, top, b, b, ord);
-        pick = ord[k - 1 - m.pre_cnt[b]];
+        if (m.pre_cnt[b + 1] - m.pre_cnt[b] > (uint32_t) CAP) {
+            const uint64_t runk = gather_run<T, B>(r, m, top, b);
+            if (!runk) return -1;
+            pick = ((runk - 1) << 32) | (uint64_t) ((const uint32_t *) m.ent)[k - 1 - m.pre_cnt[b]];
+        } else {
+            gather_in_order<T, B>(r, m, top, b, b, ord);
+            pick = ord[k - 1 - m.pre_cnt[b]];
+        }
     }
     if (tid == 0) {
         write_row(a, row, (int) entry_id(pick), SPX_ROW_OK, (int) k);
@@ -2402,7 +2467,8 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
         if (ng > CAP && one_key) {
             // A run of ng equal tokens (bfloat16 logits make long ones): each weighs the same, so the target's place
             // in the run is arithmetic, and the run's order is the tokens' order by id; the token at that place is
-            // found by a count over id ranges and a read that gathers one range.
+            // found by a read that gathers the run's ids (up to twice CAP, as 32-bit words), or by a count over id
+            // ranges and a read that gathers one range.
             const uint32_t key = (uint32_t) (one_key - 1);
             const float qk = key_float(key);
             const uint64_t m1 = qk > -INFINITY ? fixed_mass(qk, top, shift) : 0ull;
@@ -2412,6 +2478,28 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             else if (Q.kind == kQGe) j = Q.lo == 0 ? 0 : (Q.lo - base_m + m1 - 1) / m1 - 1;
             else j = (Q.lo - base_m) / m1;
             if (j >= (uint64_t) ng) return false;
+            if (ng <= 2 * CAP) {
+                // the entries' low words (the ids complemented) of the whole run, sorted falling: ids rising
+                uint32_t * gid = (uint32_t *) m.ent;  // CAP entries hold 2 x CAP words
+                if (tid == 0) m.n_gath = 0u;
+                __syncthreads();
+                fb_visit<T, B>(r, [&](uint64_t e, float, float qq, bool banned, int) {
+                    if (!in_bin(e, qq, banned) || entry_key(e) != key) return;
+                    const uint32_t at = atomicAdd(&m.n_gath, 1u);
+                    if (at < (uint32_t) (2 * CAP)) gid[at] = (uint32_t) e;
+                });
+                __syncthreads();
+                if ((int) m.n_gath != ng) return false;  // the run is the sub-bin's tokens: a count that differs is no run
+                block_sort_desc<B, uint32_t>(gid, ng);
+                const uint64_t entry = ((uint64_t) key << 32) | (uint64_t) gid[j];
+                __syncthreads();
+                Q.done = true;
+                Q.entry = entry;
+                Q.rank = (uint32_t) (base_c + j);
+                Q.before = base_m + j * m1;
+                Q.through = Q.before + m1;
+                return true;
+            }
             auto idbin = [&](int id) { return (int) (((uint64_t) id * (uint64_t) SNB) / (uint64_t) a.vocab); };
             for (int x = tid; x <= SNB; x += B) scnt[x] = 0u;
             __syncthreads();

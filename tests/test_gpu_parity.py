@@ -228,6 +228,32 @@ def test_bf16_runs_of_equal_logits(sampler):
     check(sampler, w)
 
 
+@pytest.mark.parametrize("run", [6000, 20000])
+def test_runs_longer_than_a_read(sampler, run):
+    # A run of equal bfloat16 logits longer than a gathering read takes, with the top-p cut and the pick inside it:
+    # up to twice that length the run's ids are gathered in one read, beyond it an id range is counted first. FISH and
+    # Haru order a run by id, so the token at each place is exact. Haru's float32 running sum steps through a run of up
+    # to twice a read's tokens; a longer one takes the radix path, whose Haru weights use the exact sum, so Haru rows
+    # are in the shorter case only.
+    spx = workloads.spx_module()
+    rng = np.random.default_rng(37 + run)
+    rows, vocab = 6, 151936
+    x = np.full((rows, vocab), -30.0, dtype=np.float32)
+    for r in range(rows):
+        pos = rng.permutation(vocab)
+        x[r, pos[:1000]] = 2.0
+        x[r, pos[1000:1000 + run]] = 0.0
+    logits = workloads.to_bf16_bits(x)
+    flavor = np.array([2, 2, 2, 1, 1, 0]) if run <= 8192 else np.array([2, 2, 2, 2, 0, 0])
+    p = spx.row_params(rows, flavor=flavor, temperature=1.0, top_k=0,
+                       top_p=np.array([0.9, 0.99, 0.75, 0.9, 1.0, 0.9], dtype=np.float32))
+    # u past the 2.0 tokens' share, so that the picks land in the run too
+    u = np.array([0.7, 0.95, 0.8, 0.75, 0.9, 0.6])
+    w = workloads.Workload(name=f"run {run}", logits=logits, dtype="bf16", params=p, u=u, hist=None, hist_off=None,
+                           banned=None, banned_stride=0)
+    check(sampler, w)
+
+
 def test_repeated_calls_reuse_workspace(sampler):
     # The per-row counters and the fallback list reset themselves: calls in a row give the same answers.
     w = workloads.make("mixed", rows=64, seed=21)
