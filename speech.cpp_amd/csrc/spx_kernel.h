@@ -2337,6 +2337,32 @@ __device__ __forceinline__ bool wide_row(const Launch & a, int row, const spx_ro
             Q.rank = ~0u;
             return true;
         }
+        if constexpr (sizeof(T) == 2) {
+            // bfloat16 logits crowd a bin with one value: a read of the run's ids answers the question (each token
+            // weighs the same, so the target's place is arithmetic, and the run's order is by id)
+            const uint64_t runk = gather_run<T, B>(r, m, top, b);
+            if (runk) {
+                const uint32_t key = (uint32_t) (runk - 1);
+                const float qk = key_float(key);
+                const uint64_t m1 = qk > -INFINITY ? fixed_mass(qk, top, shift) : 0ull;
+                const uint64_t base_c = m.pre_cnt[b], base_m = m.pre_mass[b];
+                const uint64_t ng = m.pre_cnt[b + 1] - m.pre_cnt[b];
+                uint64_t j;
+                if (Q.kind == kQRank) j = Q.lo - base_c;
+                else if (m1 == 0) j = 0;
+                else if (Q.kind == kQGe) j = Q.lo == 0 ? 0 : (Q.lo - base_m + m1 - 1) / m1 - 1;
+                else j = (Q.lo - base_m) / m1;
+                if (j >= ng) return false;
+                const uint64_t entry = ((uint64_t) key << 32) | (uint64_t) ((const uint32_t *) m.ent)[j];
+                __syncthreads();
+                Q.done = true;
+                Q.entry = entry;
+                Q.rank = (uint32_t) (base_c + j);
+                Q.before = base_m + j * m1;
+                Q.through = Q.before + m1;
+                return true;
+            }
+        }
         auto sub_of = [&](float qq, int id) {
             if (b == NB) return (int) (((uint64_t) id * (uint64_t) SNB) / (uint64_t) a.vocab);
             const float x = (top - qq) * kWideScale - (float) b;
