@@ -1874,12 +1874,13 @@ __device__ __forceinline__ void gather_in_order(FbRow & r, WideMem<NB, CAP> & m,
 
 // The tokens of bin b (a finite bin before the last) when they are a run of one value, at most 2 x CAP of them: their
 // entries' low words (the ids complemented) sorted falling, so ids rising, which is the row's order, in the words at
-// m.ent. Returns the run's key + 1, or 0 when the bin holds more tokens or more than one value.
+// m.ent. Returns the run's key + 1, or 0 when the bin holds more than one value, or more than 2 x CAP tokens. With
+// any_len a longer run is found too, its ids not kept.
 template <typename T, int B, int NB, int CAP>
-__device__ __forceinline__ uint64_t gather_run(FbRow & r, WideMem<NB, CAP> & m, float top, int b) {
+__device__ __forceinline__ uint64_t gather_run(FbRow & r, WideMem<NB, CAP> & m, float top, int b, bool any_len = false) {
     const int tid = threadIdx.x;
     const uint32_t n = m.pre_cnt[b + 1] - m.pre_cnt[b];
-    if (b >= NB - 1 || n > (uint32_t) (2 * CAP)) return 0;
+    if (b >= NB - 1 || (n > (uint32_t) (2 * CAP) && !any_len)) return 0;
     uint32_t * gid = (uint32_t *) m.ent;
     uint32_t * kr = (uint32_t *) m.wb;  // the bin's smallest and largest key
     if (tid == 0) {
@@ -1907,7 +1908,7 @@ __device__ __forceinline__ uint64_t gather_run(FbRow & r, WideMem<NB, CAP> & m, 
     const uint32_t key = kr[0];
     __syncthreads();
     if (!run) return 0;
-    block_sort_desc<B, uint32_t>(gid, (int) n);
+    if (n <= (uint32_t) (2 * CAP)) block_sort_desc<B, uint32_t>(gid, (int) n);
     return (uint64_t) key + 1;
 }
 
@@ -1949,7 +1950,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                 if (haru_exp(qhi, top) < half_ulp(sumf)) break;
             }
             int b1 = batch_end(m, b0);
-            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0) : 0;
+            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0, true) : 0;  // the sum needs no ids
             if (b1 < 0 && !runk) return -1;
             if (runk) b1 = b0;
             else gather_in_order<T, B>(r, m, top, b0, b1, ord);
@@ -1996,6 +1997,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
         dsh[1] = 0.0;
         ush[0] = 0;
         ush[1] = 0;
+        ush[2] = 0;  // a place the sweeps need lies in a run whose ids are not kept
     }
     __syncthreads();
     for (int sweep = 0; sweep < 2; sweep++) {
@@ -2004,12 +2006,15 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
         bool stop = false;
         while (!stop && b0 <= NB && m.pre_cnt[b0] < k) {
             int b1 = batch_end(m, b0);
-            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0) : 0;
+            const uint64_t runk = b1 < 0 ? gather_run<T, B>(r, m, top, b0, true) : 0;
             if (b1 < 0 && !runk) return -1;
             if (runk) b1 = b0;
             else gather_in_order<T, B>(r, m, top, b0, b1, ord);
             const uint32_t base = m.pre_cnt[b0];
             const int n = (int) (m.pre_cnt[b1 + 1] - base);
+            // a run longer than 2 x CAP keeps no ids: the weights run through it, but a listed candidate or the pick
+            // inside it sends the row to the radix path
+            const bool ids = !runk || n <= 2 * CAP;
             if (tid == 0) {
                 // the batch's entry at place i: a run's from its sorted ids
                 const uint32_t * gid = (const uint32_t *) m.ent;
@@ -2033,6 +2038,11 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                     if (sweep == 0) {
                         total += w;
                         if (rank < (uint64_t) nl) {
+                            if (!ids) {
+                                ush[2] = 1;
+                                st = true;
+                                break;
+                            }
                             a.out_cand_ids[(int64_t) row * a.max_out + (int64_t) rank] = (int32_t) entry_id(at(i));
                             a.out_cand_w[(int64_t) row * a.max_out + (int64_t) rank] = w;
                         }
@@ -2041,8 +2051,12 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
                         // src/common/sampling.cpp:9-19 over the k weights; its last is the k-th token
                         share += w / total;
                         if (rank + 1 < k && share > u) {
-                            ush[0] = 1;
-                            ush[1] = at(i);
+                            if (ids) {
+                                ush[0] = 1;
+                                ush[1] = at(i);
+                            } else {
+                                ush[2] = 1;
+                            }
                             st = true;
                         } else if (zero && cum >= stop_at) {
                             st = true;  // every later weight is 0: the share rises no more
@@ -2056,6 +2070,7 @@ __device__ __forceinline__ int haru_exact(const Launch & a, int row, const Plan 
             }
             __syncthreads();
             stop = sh[1] != 0.0f;
+            if (ush[2]) return -1;  // every thread reads it before any writes it again
             __syncthreads();
             b0 = b1 + 1;
         }

@@ -232,9 +232,10 @@ def test_bf16_runs_of_equal_logits(sampler):
 def test_runs_longer_than_a_read(sampler, run):
     # A run of equal bfloat16 logits longer than a gathering read takes, with the top-p cut and the pick inside it:
     # up to twice that length the run's ids are gathered in one read, beyond it an id range is counted first. FISH and
-    # Haru order a run by id, so the token at each place is exact. Haru's float32 running sum steps through a run of up
-    # to twice a read's tokens; a longer one takes the radix path, whose Haru weights use the exact sum, so Haru rows
-    # are in the shorter case only.
+    # Haru order a run by id, so the token at each place is exact. Haru's float32 running sums step through a run of
+    # any length, but keep its ids only up to twice a read's tokens: a Haru pick or listed candidate inside a longer
+    # run takes the radix path, whose Haru weights use the exact sum, so the longer case has Haru rows whose pick and
+    # listed candidates lie before the run (u below the top tokens' share).
     spx = workloads.spx_module()
     rng = np.random.default_rng(37 + run)
     rows, vocab = 6, 151936
@@ -244,11 +245,12 @@ def test_runs_longer_than_a_read(sampler, run):
         x[r, pos[:1000]] = 2.0
         x[r, pos[1000:1000 + run]] = 0.0
     logits = workloads.to_bf16_bits(x)
-    flavor = np.array([2, 2, 2, 1, 1, 0]) if run <= 8192 else np.array([2, 2, 2, 2, 0, 0])
-    p = spx.row_params(rows, flavor=flavor, temperature=1.0, top_k=0,
+    p = spx.row_params(rows, flavor=np.array([2, 2, 2, 1, 1, 0]), temperature=1.0, top_k=0,
                        top_p=np.array([0.9, 0.99, 0.75, 0.9, 1.0, 0.9], dtype=np.float32))
-    # u past the 2.0 tokens' share, so that the picks land in the run too
+    # u past the 2.0 tokens' share, so that the picks land in the run too (but for the Haru rows of the longer run)
     u = np.array([0.7, 0.95, 0.8, 0.75, 0.9, 0.6])
+    if run > 8192:
+        u[3:5] = 0.1
     w = workloads.Workload(name=f"run {run}", logits=logits, dtype="bf16", params=p, u=u, hist=None, hist_off=None,
                            banned=None, banned_stride=0)
     check(sampler, w)
